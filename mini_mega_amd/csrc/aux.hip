@@ -1,0 +1,180 @@
+// aux.hip -- data-preparation kernels: deterministic and synthetic weight
+// generators in the tile layout, logical -> tile packing, bf16 -> fp8
+// activation cast, a conversion self-test, the empty kernel and a fill.
+#include "mm_kernels.h"
+
+namespace mm {
+
+// Slot s (16 bytes) of a tile holds row r = L%16, k = 32*(L/16) + 16*h + [0,16)
+// with h = s / 64, L = s % 64 (the inverse of tile_byte()).
+__device__ __forceinline__ void slot_coords(size_t i, int KT, int& row, int& k) {
+    const size_t tile = i >> 7;
+    const int s = (int)(i & 127);
+    const int h = s >> 6, L = s & 63;
+    const int nt = (int)(tile / KT), kt = (int)(tile % KT);
+    row = nt * 16 + (L & 15);
+    k = kt * 128 + 32 * (L >> 4) + 16 * h;
+}
+
+// Reference: fill_w_lane_kernel, src/megakernel.cu:66-105 (same value
+// function, this library's tile layout).
+__global__ void __launch_bounds__(256)
+fill_w_lane_kernel(uint8_t* __restrict__ w, int n_rows, int k_cols, uint32_t seed) {
+    const int KT = k_cols >> 7;
+    const size_t total = (size_t)(n_rows >> 4) * KT * 128;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        int row, k;
+        slot_coords(i, KT, row, k);
+        v4i v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                word |= (uint32_t)WPROBE_VAL(seed, (uint32_t)row, (uint32_t)(k + 4 * q + b))
+                        << (8 * b);
+            v[q] = (int)word;
+        }
+        *reinterpret_cast<v4i*>(w + i * 16) = v;
+    }
+}
+
+// Logical row-major [n_mats][n_rows][k_cols] -> tile layout, 16 bytes per thread.
+__global__ void __launch_bounds__(256)
+pack_weights_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, int n_mats,
+                    int n_rows, int k_cols) {
+    const int KT = k_cols >> 7;
+    const size_t per_mat = (size_t)(n_rows >> 4) * KT * 128;
+    const size_t total = per_mat * n_mats;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t m = i / per_mat, j = i % per_mat;
+        int row, k;
+        slot_coords(j, KT, row, k);
+        const uint8_t* s = src + (m * n_rows + row) * (size_t)k_cols + k;
+        *reinterpret_cast<v4i*>(dst + i * 16) = *reinterpret_cast<const v4i*>(s);
+    }
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// Standard normal from a 64-bit hash (Box-Muller, cosine branch).
+__device__ __forceinline__ float hash_normal(uint64_t key) {
+    const uint64_t h = splitmix64(key);
+    const float u1 = ((float)(uint32_t)(h >> 32) + 1.0f) * 2.3283064365386963e-10f;  // (0,1]
+    const float u2 = (float)(uint32_t)h * 2.3283064365386963e-10f;                   // [0,1)
+    return sqrtf(-2.0f * __logf(u1)) * __cosf(6.283185307179586f * u2);
+}
+
+// Synthetic N(0, sigma) weights with 128x128 UE8M0 block scales
+// (torch/mxmegakernel/utils/math.py:62-72 recipe).  One workgroup per
+// (128 k-block, 128 row-block, matrix); each thread makes 4 slots = 64 values.
+__global__ void __launch_bounds__(256)
+fill_weights_normal_kernel(uint8_t* __restrict__ w, uint8_t* __restrict__ w_sf, int n_rows,
+                           int k_cols, uint64_t seed, float sigma) {
+    const int KT = k_cols >> 7;
+    const int kb = blockIdx.x, rb = blockIdx.y, m = blockIdx.z;
+    __shared__ float red[4];
+    float v[4][16];
+    float amax = 0.0f;
+    // tiles of this block: nt = rb*8 .. rb*8+7 at kt = kb; slot index inside the
+    // block: q = threadIdx.x + 256*u (1024 slots = 8 tiles x 128 slots)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int q = threadIdx.x + 256 * u;
+        const int nt = rb * 8 + (q >> 7);
+        const size_t slot = ((size_t)nt * KT + kb) * 128 + (q & 127);
+        int row, k;
+        slot_coords(slot, KT, row, k);
+        const uint64_t base = ((uint64_t)m * n_rows + row) * (uint64_t)k_cols + k;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            v[u][b] = sigma * hash_normal(seed * 0x100000001B3ull + base + b);
+            amax = fmaxf(amax, fabsf(v[u][b]));
+        }
+    }
+    for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const uint32_t sb = block_scale_byte(amax);
+    const float inv = inv_scale(sb);
+    if (threadIdx.x == 0) w_sf[((size_t)m * (n_rows >> 7) + rb) * KT + kb] = (uint8_t)sb;
+    uint8_t* wm = w + (size_t)m * n_rows * (size_t)k_cols;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int q = threadIdx.x + 256 * u;
+        const int nt = rb * 8 + (q >> 7);
+        const size_t slot = ((size_t)nt * KT + kb) * 128 + (q & 127);
+        v4i o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            o[c] = (int)pack4_fp8(v[u][4 * c] * inv, v[u][4 * c + 1] * inv,
+                                  v[u][4 * c + 2] * inv, v[u][4 * c + 3] * inv);
+        *reinterpret_cast<v4i*>(wm + slot * 16) = o;
+    }
+}
+
+// bf16 [rows][cols] -> fp8; sf != null: per-row per-128 UE8M0
+// (utils/math.py:23-47); sf == null: RNE saturating cast (x_fold_body,
+// src/prologue.cuh:103-122).  8 elements per thread, 16 threads per block.
+__global__ void __launch_bounds__(256)
+quant_act_kernel(const uint16_t* __restrict__ x, int rows, int cols, uint8_t* __restrict__ q,
+                 uint8_t* __restrict__ sf) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t n8 = (size_t)rows * cols / 8;
+    const bool in = i < n8;
+    float v[8];
+    if (in) {
+        const v4i raw = *reinterpret_cast<const v4i*>(x + i * 8);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[2 * c] = bf16_to_f32((uint32_t)raw[c] & 0xFFFFu);
+            v[2 * c + 1] = bf16_to_f32((uint32_t)raw[c] >> 16);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = 0.0f;
+    }
+    float inv = 1.0f;
+    if (sf) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) amax = fmaxf(amax, fabsf(v[c]));
+        for (int d = 8; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 16));
+        const uint32_t sb = block_scale_byte(amax);
+        inv = inv_scale(sb);
+        if (in && (threadIdx.x & 15) == 0) sf[i / 16] = (uint8_t)sb;
+    }
+    if (in) {
+        uint2 o;
+        o.x = pack4_fp8(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+        o.y = pack4_fp8(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        *reinterpret_cast<uint2*>(q + i * 8) = o;
+    }
+}
+
+__global__ void __launch_bounds__(256)
+convert_selftest_kernel(const float* __restrict__ in, int n, uint8_t* __restrict__ out8,
+                        uint16_t* __restrict__ out16) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = in[i];
+    if (out8) out8[i] = (uint8_t)(pack4_fp8(v, 0.f, 0.f, 0.f) & 0xFFu);
+    if (out16) out16[i] = (uint16_t)bf16_rne(v);
+}
+
+__global__ void empty_kernel() {}
+
+__global__ void __launch_bounds__(256) fill_int_kernel(int* p, int n, int v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+}  // namespace mm

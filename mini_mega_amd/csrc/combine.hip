@@ -1,0 +1,52 @@
+// combine.hip -- top-k weighted reduce of the L2 rows back into token order
+// (reference: reduce_tile_body src/combine.cuh:488-641; host model ref_reduce
+// src/bench_check.cuh:484-499):
+//   y[t][c] = sum_{k = 0..topk-1, in order} bf16->f32(l2[pair_pos[t,k]][c]) * w[t][k]
+// in fp32, product then add (no fused multiply-add, so the sum is bitwise the
+// reference's sequential loop); pairs without a slot (invalid expert id or
+// over the slot cap) contribute nothing.  Each thread owns 8 channels (one
+// 16-byte bf16 load per k), no atomics: the output is deterministic.
+#include "mm_kernels.h"
+
+namespace mm {
+
+__global__ void __launch_bounds__(256)
+combine_kernel(const uint16_t* __restrict__ l2, const int* __restrict__ pair_pos,
+               const float* __restrict__ w, int topk, int H, float* __restrict__ y,
+               uint16_t* __restrict__ y_bf16) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x;
+    const int c0 = (blockIdx.y * blockDim.x + threadIdx.x) * 8;
+    if (c0 >= H) return;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int k = 0; k < topk; ++k) {
+        const int pos = pair_pos[(size_t)t * topk + k];
+        if (pos < 0) continue;
+        const float wv = w[(size_t)t * topk + k];
+        const v4i raw = load16(reinterpret_cast<const uint8_t*>(l2 + (size_t)pos * H + c0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t u = (uint32_t)raw[i];
+            const float lo = bf16_to_f32(u & 0xFFFFu) * wv;
+            const float hi = bf16_to_f32(u >> 16) * wv;
+            acc[2 * i] = acc[2 * i] + lo;
+            acc[2 * i + 1] = acc[2 * i + 1] + hi;
+        }
+    }
+    if (y) {
+        float4* yo = reinterpret_cast<float4*>(y + (size_t)t * H + c0);
+        yo[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        yo[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+    if (y_bf16) {
+        v4i o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            o[i] = (int)(bf16_rne(acc[2 * i]) | (bf16_rne(acc[2 * i + 1]) << 16));
+        *reinterpret_cast<v4i*>(y_bf16 + (size_t)t * H + c0) = o;
+    }
+}
+
+}  // namespace mm

@@ -1,0 +1,432 @@
+// megakernel.hip -- host side of the public API (include/megakernel.h): shape
+// validation, workspace layout, stream-ordered kernel launches, and the thin
+// extern "C" layer.  Reference counterpart: src/megakernel.cu:1-284 (launch
+// entry points) and test/mega_common.cuh:69-88,344-376 (geometry / args).
+//
+// Nothing here allocates, synchronises or reads the environment: every entry
+// point only validates its arguments and enqueues kernels on `stream`, so the
+// whole layer is capture-safe.  The workspace is caller-owned.
+#include <cstddef>
+#include <cstdio>
+#include <cstring>
+
+#include "mm_kernels.h"
+
+namespace fp8mega {
+namespace {
+
+thread_local int g_last_error = kOk;
+
+inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+int auto_m_tile(int tokens, int topk, int E) {
+    // Rows per work item: one item per expert when the expected expert load
+    // fits, so that each expert's weights stream from HBM once.
+    const double mean = (double)tokens * topk / (E > 0 ? E : 1);
+    if (mean <= 20.0) return 32;
+    return 64;
+}
+
+int m_tile_of(const MegaLaunchArgs& a) {
+    return a.win_cap > 0 ? a.win_cap : auto_m_tile(a.max_tokens, a.topk, a.num_experts);
+}
+
+int pairing_block(int I) { return I < 256 ? I : 256; }
+
+int check_dims(int topk, int E, int H, int I, int win_cap) {
+    if (topk < 1 || topk > 64 || E < 1 || E > mm::kMaxExperts) return kErrBadDims;
+    if (H < 256 || H % 256 != 0 || I < 128 || I % 128 != 0) return kErrBadDims;
+    if (I % pairing_block(I) != 0) return kErrBadDims;
+    if (win_cap != 0 && win_cap != 16 && win_cap != 32 && win_cap != 64) return kErrBadDims;
+    return kOk;
+}
+
+struct Bound {
+    const uint8_t* x = nullptr;
+    const uint8_t* x_sf = nullptr;
+    const float* w = nullptr;
+    MegaLayout L{};
+    uint8_t* ws = nullptr;
+    int m_tile = 32;
+};
+
+int bind(const MegaLaunchArgs& a, Bound& b, bool need_weights) {
+    int st = check_dims(a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
+    if (st != kOk) return st;
+    if (a.rwk == nullptr || a.topk_idx == nullptr || a.self == nullptr) return kErrNullPointer;
+    if (need_weights && (a.w1 == nullptr || a.w2 == nullptr)) return kErrNullPointer;
+    if (a.tokens < 0 || a.max_tokens <= 0) return kErrBadDims;
+    if (a.tokens > a.max_tokens) return kErrTooManyTokens;
+    if (a.R != 1 || a.rank != 0) return kErrUnsupported;
+    const bool any_sf = a.x_sf || a.w1_sf || a.w2_sf;
+    if (any_sf && !(a.w1_sf && a.w2_sf)) return kErrNullPointer;
+    if (any_sf && !a.in_bf16 && !a.x_sf) return kErrNullPointer;
+    b.L = layout(a.max_tokens, a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
+    if (a.workspace_bytes < b.L.total) return kErrWorkspace;
+    b.ws = reinterpret_cast<uint8_t*>(a.rwk);
+    b.x = a.self + a.x_off;
+    b.x_sf = a.x_sf;
+    b.w = reinterpret_cast<const float*>(a.self + a.weights_off);
+    b.m_tile = b.L.m_tile;
+    if (a.in_bf16) {
+        b.x = b.ws + b.L.xq;
+        b.x_sf = a.w1_sf ? b.ws + b.L.xq_sf : nullptr;
+    }
+    return kOk;
+}
+
+template <class T>
+T* at(const Bound& b, int64_t off) { return reinterpret_cast<T*>(b.ws + off); }
+
+int launched(int st) {
+    if (st != kOk) return st;
+    return hipPeekAtLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int do_prelude(const MegaLaunchArgs& a, hipStream_t s) {
+    Bound b;
+    int st = bind(a, b, false);
+    if (st != kOk) return st;
+    const int E = a.num_experts, P = a.tokens * a.topk;
+    int* status = at<int>(b, b.L.status);
+    hipLaunchKernelGGL(mm::fill_int_kernel, dim3(1), dim3(256), 0, s, status, 16, 0);
+    if (a.in_bf16) {
+        const size_t n8 = (size_t)a.tokens * a.hidden / 8;
+        if (n8 > 0)
+            hipLaunchKernelGGL(mm::quant_act_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256),
+                               0, s, reinterpret_cast<const uint16_t*>(a.self + a.x_off),
+                               a.tokens, a.hidden, b.ws + b.L.xq,
+                               a.w1_sf ? b.ws + b.L.xq_sf : nullptr);
+    }
+    const int nchunks = P > 0 ? (P + mm::kRouteChunk - 1) / mm::kRouteChunk : 0;
+    int* hist = at<int>(b, b.L.chunk_hist);
+    if (nchunks > 0)
+        hipLaunchKernelGGL(mm::route_hist_kernel, dim3(nchunks), dim3(mm::kRouteThreads), 0, s,
+                           a.topk_idx, P, E, hist);
+    const int cap = a.slot_capacity > 0 ? a.slot_capacity : (P > 0 ? P : 1);
+    hipLaunchKernelGGL(mm::route_scan_kernel, dim3(1), dim3(mm::kScanThreads), 0, s, hist,
+                       nchunks, E, cap, b.m_tile, b.L.max_items, at<int>(b, b.L.counts),
+                       at<int>(b, b.L.offsets), at<int>(b, b.L.items), status);
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+    if (nchunks > 0)
+        hipLaunchKernelGGL(mm::route_scatter_kernel, dim3(nchunks), dim3(mm::kRouteThreads), 0,
+                           s, a.topk_idx, P, E, nbits, hist, at<int>(b, b.L.counts),
+                           at<int>(b, b.L.offsets), at<uint32_t>(b, b.L.perm),
+                           at<int>(b, b.L.pair_pos));
+    return launched(kOk);
+}
+
+mm::GemmParams gemm_params(const MegaLaunchArgs& a, const Bound& b) {
+    mm::GemmParams p{};
+    p.counts = at<int>(b, b.L.counts);
+    p.offsets = at<int>(b, b.L.offsets);
+    p.items = at<int>(b, b.L.items);
+    p.status = at<int>(b, b.L.status);
+    p.perm = at<uint32_t>(b, b.L.perm);
+    p.H = a.hidden;
+    p.I = a.intermediate;
+    p.G = pairing_block(a.intermediate);
+    p.topk = a.topk;
+    p.ffn_ue8m0 = a.ffn_ue8m0;
+    return p;
+}
+
+void launch_gemm(void (*k1)(mm::GemmParams), void (*k2)(mm::GemmParams),
+                 void (*k4)(mm::GemmParams), int m_tile, dim3 grid, hipStream_t s,
+                 const mm::GemmParams& p) {
+    void (*k)(mm::GemmParams) = m_tile <= 16 ? k1 : (m_tile <= 32 ? k2 : k4);
+    hipLaunchKernelGGL(k, grid, dim3(mm::kGemmThreads), 0, s, p);
+}
+
+int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
+    Bound b;
+    int st = bind(a, b, true);
+    if (st != kOk) return st;
+    if (a.tokens == 0) return kOk;
+    mm::GemmParams p = gemm_params(a, b);
+    p.x = b.x;
+    p.x_sf = b.x_sf;
+    p.w = a.w1;
+    p.w_sf = a.w1_sf;
+    p.out8 = b.ws + b.L.ffn;
+    p.out_sf = b.ws + b.L.ffn_sf;
+    const dim3 grid(a.intermediate / mm::kL1BlockH, b.L.max_items);
+    launch_gemm(mm::l1_kernel<1>, mm::l1_kernel<2>, mm::l1_kernel<4>, b.m_tile, grid, s, p);
+    return launched(kOk);
+}
+
+int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
+    Bound b;
+    int st = bind(a, b, true);
+    if (st != kOk) return st;
+    if (a.tokens == 0) return kOk;
+    mm::GemmParams p = gemm_params(a, b);
+    p.x = b.ws + b.L.ffn;
+    p.x_sf = a.ffn_ue8m0 ? b.ws + b.L.ffn_sf : nullptr;
+    p.w = a.w2;
+    p.w_sf = a.w2_sf;
+    p.out16 = at<uint16_t>(b, b.L.l2);
+    const dim3 grid(a.hidden / mm::kL2BlockN, b.L.max_items);
+    launch_gemm(mm::l2_kernel<1>, mm::l2_kernel<2>, mm::l2_kernel<4>, b.m_tile, grid, s, p);
+    return launched(kOk);
+}
+
+int do_reduce(const MegaLaunchArgs& a, hipStream_t s) {
+    Bound b;
+    int st = bind(a, b, false);
+    if (st != kOk) return st;
+    if (a.y == nullptr && a.y_bf16 == nullptr) return kErrNullPointer;
+    if (a.skip_combine || a.tokens == 0) return kOk;
+    const int per_block = 256 * 8;
+    const dim3 grid(a.tokens, (a.hidden + per_block - 1) / per_block);
+    hipLaunchKernelGGL(mm::combine_kernel, grid, dim3(256), 0, s, at<uint16_t>(b, b.L.l2),
+                       at<int>(b, b.L.pair_pos), b.w, a.topk, a.hidden, a.y, a.y_bf16);
+    return launched(kOk);
+}
+
+int do_compute(const MegaLaunchArgs& a, hipStream_t s) {
+    int st = kOk;
+    if (!a.skip_prologue) st = do_prelude(a, s);
+    if (st == kOk) st = do_l1(a, s);
+    if (st == kOk) st = do_l2(a, s);
+    return st;
+}
+
+int do_full(const MegaLaunchArgs& a, hipStream_t s) {
+    int st = do_compute(a, s);
+    if (st == kOk) st = do_reduce(a, s);
+    return st;
+}
+
+int do_dispatch(const MegaLaunchArgs& a, uint8_t* pool, hipStream_t s) {
+    Bound b;
+    int st = bind(a, b, false);
+    if (st != kOk) return st;
+    if (pool == nullptr) return kErrNullPointer;
+    const int P = a.tokens * a.topk;
+    if (P == 0) return kOk;
+    hipLaunchKernelGGL(mm::dispatch_gather_kernel, dim3(P), dim3(256), 0, s, b.x, a.hidden,
+                       a.topk, at<uint32_t>(b, b.L.perm), at<int>(b, b.L.status), pool);
+    return launched(kOk);
+}
+
+int record(int st) {
+    g_last_error = st;
+    if (st != kOk) std::fprintf(stderr, "[fp8mega] error %d\n", st);
+    return st;
+}
+
+unsigned grid_for(size_t n, unsigned cap = 1u << 16) {
+    size_t g = (n + 255) / 256;
+    if (g < 1) g = 1;
+    return (unsigned)(g > cap ? cap : g);
+}
+
+}  // namespace
+
+MegaLayout layout(int max_tokens, int topk, int num_experts, int hidden, int intermediate,
+                  int win_cap) {
+    MegaLayout L{};
+    const int64_t P = (int64_t)(max_tokens > 0 ? max_tokens : 1) * topk;
+    const int64_t E = num_experts;
+    L.max_pairs = (int)P;
+    L.nchunks = (int)((P + mm::kRouteChunk - 1) / mm::kRouteChunk);
+    L.m_tile = win_cap > 0 ? win_cap : auto_m_tile(max_tokens, topk, num_experts);
+    L.max_items = (int)((P + L.m_tile - 1) / L.m_tile + E);
+    int64_t o = 0;
+    L.status = o;      o = align256(o + 16 * 4);
+    L.chunk_hist = o;  o = align256(o + (int64_t)L.nchunks * E * 4);
+    L.counts = o;      o = align256(o + E * 4);
+    L.offsets = o;     o = align256(o + (E + 1) * 4);
+    L.items = o;       o = align256(o + (int64_t)L.max_items * 8);
+    L.perm = o;        o = align256(o + P * 4);
+    L.pair_pos = o;    o = align256(o + P * 4);
+    L.xq = o;          o = align256(o + (int64_t)max_tokens * hidden);
+    L.xq_sf = o;       o = align256(o + (int64_t)max_tokens * (hidden / 128));
+    L.ffn = o;         o = align256(o + P * intermediate);
+    L.ffn_sf = o;      o = align256(o + P * (intermediate / 128));
+    L.l2 = o;          o = align256(o + P * hidden * 2);
+    L.total = o;
+    return L;
+}
+
+void launch_prelude(const MegaLaunchArgs& a, hipStream_t s) { record(do_prelude(a, s)); }
+void launch_compute(const MegaLaunchArgs& a, hipStream_t s) { record(do_compute(a, s)); }
+void launch_l1(const MegaLaunchArgs& a, hipStream_t s) { record(do_l1(a, s)); }
+void launch_l2(const MegaLaunchArgs& a, hipStream_t s) { record(do_l2(a, s)); }
+void launch_reduce(const MegaLaunchArgs& a, hipStream_t s) { record(do_reduce(a, s)); }
+void launch_full(const MegaLaunchArgs& a, hipStream_t s) { record(do_full(a, s)); }
+void launch_dispatch(const MegaLaunchArgs& a, uint8_t* pool, hipStream_t s) {
+    record(do_dispatch(a, pool, s));
+}
+
+void launch_empty(int grid, int threads, int64_t smem, hipStream_t s) {
+    hipLaunchKernelGGL(mm::empty_kernel, dim3(grid > 0 ? grid : 1),
+                       dim3(threads > 0 ? threads : 64), (unsigned)smem, s);
+    record(launched(kOk));
+}
+
+void fill_weights_lane(uint8_t* w, int n_rows, int k_cols, uint32_t seed, hipStream_t s) {
+    if (w == nullptr) { record(kErrNullPointer); return; }
+    if (n_rows <= 0 || n_rows % 16 || k_cols <= 0 || k_cols % 128) { record(kErrBadDims); return; }
+    const size_t slots = (size_t)(n_rows / 16) * (k_cols / 128) * 128;
+    hipLaunchKernelGGL(mm::fill_w_lane_kernel, dim3(grid_for(slots)), dim3(256), 0, s, w, n_rows,
+                       k_cols, seed);
+    record(launched(kOk));
+}
+
+void pack_weights(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows, int k_cols,
+                  hipStream_t s) {
+    if (!dst || !src) { record(kErrNullPointer); return; }
+    if (n_mats <= 0 || n_rows <= 0 || n_rows % 16 || k_cols <= 0 || k_cols % 128) {
+        record(kErrBadDims);
+        return;
+    }
+    const size_t slots = (size_t)n_mats * (n_rows / 16) * (k_cols / 128) * 128;
+    hipLaunchKernelGGL(mm::pack_weights_kernel, dim3(grid_for(slots)), dim3(256), 0, s, dst, src,
+                       n_mats, n_rows, k_cols);
+    record(launched(kOk));
+}
+
+void fill_weights_normal(uint8_t* w, uint8_t* w_sf, int n_mats, int n_rows, int k_cols,
+                         uint64_t seed, float sigma, hipStream_t s) {
+    if (!w || !w_sf) { record(kErrNullPointer); return; }
+    if (n_mats <= 0 || n_rows <= 0 || n_rows % 128 || k_cols <= 0 || k_cols % 128 ||
+        n_mats > 65535 || n_rows / 128 > 65535) {
+        record(kErrBadDims);
+        return;
+    }
+    hipLaunchKernelGGL(mm::fill_weights_normal_kernel, dim3(k_cols / 128, n_rows / 128, n_mats),
+                       dim3(256), 0, s, w, w_sf, n_rows, k_cols, seed, sigma);
+    record(launched(kOk));
+}
+
+void quant_act(const uint16_t* x, int rows, int cols, uint8_t* q, uint8_t* sf, hipStream_t s) {
+    if (!x || !q) { record(kErrNullPointer); return; }
+    if (rows < 0 || cols <= 0 || cols % 128) { record(kErrBadDims); return; }
+    const size_t n8 = (size_t)rows * cols / 8;
+    if (n8 > 0)
+        hipLaunchKernelGGL(mm::quant_act_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                           s, x, rows, cols, q, sf);
+    record(launched(kOk));
+}
+
+static void print_attr(const char* name, const void* fn) {
+    hipFuncAttributes at{};
+    if (hipFuncGetAttributes(&at, fn) != hipSuccess) {
+        std::printf("[resources] %-26s (unavailable)\n", name);
+        return;
+    }
+    std::printf("[resources] %-26s regs=%3d lds=%6zu B scratch=%5zu B max_threads=%d\n", name,
+                at.numRegs, at.sharedSizeBytes, at.localSizeBytes, at.maxThreadsPerBlock);
+}
+
+void dump_kernel_resources() {
+    print_attr("route_hist", (const void*)mm::route_hist_kernel);
+    print_attr("route_scan", (const void*)mm::route_scan_kernel);
+    print_attr("route_scatter", (const void*)mm::route_scatter_kernel);
+    print_attr("l1_kernel<1>", (const void*)mm::l1_kernel<1>);
+    print_attr("l1_kernel<2>", (const void*)mm::l1_kernel<2>);
+    print_attr("l1_kernel<4>", (const void*)mm::l1_kernel<4>);
+    print_attr("l2_kernel<1>", (const void*)mm::l2_kernel<1>);
+    print_attr("l2_kernel<2>", (const void*)mm::l2_kernel<2>);
+    print_attr("l2_kernel<4>", (const void*)mm::l2_kernel<4>);
+    print_attr("combine", (const void*)mm::combine_kernel);
+    std::fflush(stdout);
+}
+
+int last_error() { return g_last_error; }
+
+}  // namespace fp8mega
+
+// ------------------------------------------------------------------ C ABI --
+using fp8mega::MegaLaunchArgs;
+
+extern "C" {
+
+int mm_abi_version(void) { return 1; }
+
+size_t mm_args_size(void) { return sizeof(MegaLaunchArgs); }
+
+long long mm_args_offset(const char* f) {
+#define MM_FIELD(n) if (std::strcmp(f, #n) == 0) return (long long)offsetof(MegaLaunchArgs, n);
+    MM_FIELD(R) MM_FIELD(rank) MM_FIELD(tokens) MM_FIELD(slot_capacity) MM_FIELD(win_cap)
+    MM_FIELD(grid) MM_FIELD(threads) MM_FIELD(smem) MM_FIELD(rwk) MM_FIELD(unk)
+    MM_FIELD(unk_peers) MM_FIELD(self) MM_FIELD(peer_bases) MM_FIELD(topk_idx) MM_FIELD(w1)
+    MM_FIELD(w2) MM_FIELD(group_weights_ready) MM_FIELD(topk_idx_off) MM_FIELD(x_off)
+    MM_FIELD(weights_off) MM_FIELD(in_bf16) MM_FIELD(skip_combine) MM_FIELD(y)
+    MM_FIELD(max_spins) MM_FIELD(skip_prologue) MM_FIELD(num_experts) MM_FIELD(topk)
+    MM_FIELD(hidden) MM_FIELD(intermediate) MM_FIELD(max_tokens) MM_FIELD(workspace_bytes)
+    MM_FIELD(x_sf) MM_FIELD(w1_sf) MM_FIELD(w2_sf) MM_FIELD(ffn_ue8m0) MM_FIELD(y_bf16)
+#undef MM_FIELD
+    return -1;
+}
+
+int mm_layout(int max_tokens, int topk, int num_experts, int hidden, int intermediate,
+              int win_cap, fp8mega::MegaLayout* out) {
+    if (!out) return fp8mega::kErrNullPointer;
+    const int st = fp8mega::check_dims(topk, num_experts, hidden, intermediate, win_cap);
+    if (st != fp8mega::kOk) return st;
+    if (max_tokens <= 0) return fp8mega::kErrBadDims;
+    *out = fp8mega::layout(max_tokens, topk, num_experts, hidden, intermediate, win_cap);
+    return fp8mega::kOk;
+}
+
+#define MM_WRAP(name, call)                                           \
+    int name(const MegaLaunchArgs* a, void* stream) {                 \
+        if (!a) return fp8mega::kErrNullPointer;                       \
+        return fp8mega::record(call(*a, (hipStream_t)stream));         \
+    }
+MM_WRAP(mm_launch_prelude, fp8mega::do_prelude)
+MM_WRAP(mm_launch_compute, fp8mega::do_compute)
+MM_WRAP(mm_launch_l1, fp8mega::do_l1)
+MM_WRAP(mm_launch_l2, fp8mega::do_l2)
+MM_WRAP(mm_launch_reduce, fp8mega::do_reduce)
+MM_WRAP(mm_launch_full, fp8mega::do_full)
+#undef MM_WRAP
+
+int mm_launch_dispatch(const MegaLaunchArgs* a, uint8_t* pool, void* stream) {
+    if (!a) return fp8mega::kErrNullPointer;
+    return fp8mega::record(fp8mega::do_dispatch(*a, pool, (hipStream_t)stream));
+}
+
+int mm_launch_empty(int grid, int threads, long long smem, void* stream) {
+    fp8mega::launch_empty(grid, threads, smem, (hipStream_t)stream);
+    return fp8mega::last_error();
+}
+
+int mm_fill_weights_lane(uint8_t* w, int n_rows, int k_cols, unsigned seed, void* stream) {
+    fp8mega::fill_weights_lane(w, n_rows, k_cols, seed, (hipStream_t)stream);
+    return fp8mega::last_error();
+}
+
+int mm_pack_weights(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows, int k_cols,
+                    void* stream) {
+    fp8mega::pack_weights(dst, src, n_mats, n_rows, k_cols, (hipStream_t)stream);
+    return fp8mega::last_error();
+}
+
+int mm_fill_weights_normal(uint8_t* w, uint8_t* w_sf, int n_mats, int n_rows, int k_cols,
+                           unsigned long long seed, float sigma, void* stream) {
+    fp8mega::fill_weights_normal(w, w_sf, n_mats, n_rows, k_cols, seed, sigma,
+                                 (hipStream_t)stream);
+    return fp8mega::last_error();
+}
+
+int mm_quant_act(const uint16_t* x, int rows, int cols, uint8_t* q, uint8_t* sf, void* stream) {
+    fp8mega::quant_act(x, rows, cols, q, sf, (hipStream_t)stream);
+    return fp8mega::last_error();
+}
+
+int mm_selftest_convert(const float* in, int n, uint8_t* out8, uint16_t* out16, void* stream) {
+    if (!in) return fp8mega::kErrNullPointer;
+    if (n <= 0) return fp8mega::kOk;
+    hipLaunchKernelGGL(mm::convert_selftest_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, in, n, out8, out16);
+    return fp8mega::record(fp8mega::launched(fp8mega::kOk));
+}
+
+void mm_dump_kernel_resources(void) { fp8mega::dump_kernel_resources(); }
+
+}  // extern "C"

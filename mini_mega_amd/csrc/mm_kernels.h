@@ -1,0 +1,57 @@
+// mm_kernels.h -- kernel declarations and launch constants shared by the
+// host launcher (megakernel.hip) and the kernel translation units.
+#pragma once
+
+#include "mm_device.h"
+#include "megakernel.h"
+
+namespace mm {
+
+constexpr int kMaxExperts = 1024;   // E upper bound (one scan thread per expert)
+constexpr int kScanThreads = 1024;
+constexpr int kRouteThreads = 256;
+constexpr int kRouteChunk = 1024;   // pairs per routing chunk
+
+constexpr int kGemmThreads = 256;   // 4 waves per workgroup
+constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 workgroup
+constexpr int kL2BlockN = 256;      // output channels per L2 workgroup
+
+// Parameters of the two grouped GEMMs (one struct so that the launcher and
+// the kernels agree on one argument list).
+struct GemmParams {
+    const uint8_t* x;         // L1: activations fp8 [tokens][H]; L2: ffn [P][I]
+    const uint8_t* x_sf;      // matching UE8M0 scales or null
+    const uint8_t* w;         // packed weights of all experts
+    const uint8_t* w_sf;      // UE8M0 block scales [E][N/128][K/128] or null
+    const int* counts;        // [E]
+    const int* offsets;       // [E+1]
+    const int* items;         // [max_items][2]
+    const int* status;        // [1] = number of items
+    const uint32_t* perm;     // slot -> pair (L1 gathers x rows through it)
+    uint8_t* out8;            // L1: ffn fp8 [P][I]
+    uint8_t* out_sf;          // L1: ffn scales [P][I/128] (ffn_ue8m0)
+    uint16_t* out16;          // L2: bf16 [P][H]
+    int H, I, G, topk;
+    int ffn_ue8m0;
+};
+
+template <int MT> __global__ void l1_kernel(GemmParams p);
+template <int MT> __global__ void l2_kernel(GemmParams p);
+
+__global__ void route_hist_kernel(const int64_t*, int, int, int*);
+__global__ void route_scan_kernel(int*, int, int, int, int, int, int*, int*, int*, int*);
+__global__ void route_scatter_kernel(const int64_t*, int, int, int, const int*, const int*,
+                                     const int*, uint32_t*, int*);
+__global__ void dispatch_gather_kernel(const uint8_t*, int, int, const uint32_t*, const int*,
+                                       uint8_t*);
+__global__ void combine_kernel(const uint16_t*, const int*, const float*, int, int, float*,
+                               uint16_t*);
+__global__ void fill_w_lane_kernel(uint8_t*, int, int, uint32_t);
+__global__ void pack_weights_kernel(uint8_t*, const uint8_t*, int, int, int);
+__global__ void fill_weights_normal_kernel(uint8_t*, uint8_t*, int, int, uint64_t, float);
+__global__ void quant_act_kernel(const uint16_t*, int, int, uint8_t*, uint8_t*);
+__global__ void convert_selftest_kernel(const float*, int, uint8_t*, uint16_t*);
+__global__ void empty_kernel();
+__global__ void fill_int_kernel(int*, int, int);
+
+}  // namespace mm

@@ -1,0 +1,175 @@
+// route.hip -- token-to-expert permutation on one GPU (the intra-GPU form of
+// the reference's EP dispatch metadata: route_build_body, src/prologue.cuh:
+// 126-226; publish_counts_body :230-256; task_setup_body :269-498).
+//
+// Three stream-ordered kernels over P = tokens * topk (token, k) pairs:
+//   1. route_hist:    per chunk of 1024 pairs, an LDS histogram over experts.
+//   2. route_scan:    one workgroup; per expert the exclusive prefix over chunks,
+//                     the capped count, the exclusive prefix over experts
+//                     (slot offsets) and the work-item list (expert, first row).
+//   3. route_scatter: per chunk, a stable rank of every pair among the pairs of
+//                     the same expert (wave ballots over the expert-id bits +
+//                     an LDS prefix across waves), giving the canonical slot
+//                     order = ascending pair index.  Writes perm[slot] and
+//                     pair_pos[pair].
+// Pairs whose id is outside [0, E) or whose rank is >= slot_capacity get
+// pair_pos = -1 (reference: dropped at route_build_body, prologue.cuh:150-175).
+#include "mm_kernels.h"
+
+namespace mm {
+
+__global__ void __launch_bounds__(kRouteThreads)
+route_hist_kernel(const int64_t* __restrict__ topk_idx, int P, int E,
+                  int* __restrict__ chunk_hist) {
+    __shared__ int hist[kMaxExperts];
+    for (int i = threadIdx.x; i < E; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    const int base = blockIdx.x * kRouteChunk;
+    const int end = min(base + kRouteChunk, P);
+    for (int p = base + threadIdx.x; p < end; p += blockDim.x) {
+        const int64_t e = topk_idx[p];
+        if (e >= 0 && e < E) atomicAdd(&hist[(int)e], 1);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < E; i += blockDim.x)
+        chunk_hist[(size_t)blockIdx.x * E + i] = hist[i];
+}
+
+// Block-wide exclusive scan of one int per thread (blockDim = kScanThreads).
+__device__ int block_exclusive_scan(int v, int* smem, int* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) smem[wave] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int w = 0; w < kScanThreads / 64; ++w) {
+            const int t = smem[w];
+            smem[w] = run;
+            run += t;
+        }
+        smem[kScanThreads / 64] = run;
+    }
+    __syncthreads();
+    const int r = smem[wave] + x - v;
+    *total = smem[kScanThreads / 64];
+    __syncthreads();
+    return r;
+}
+
+__global__ void __launch_bounds__(kScanThreads)
+route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int m_tile,
+                  int max_items, int* __restrict__ counts, int* __restrict__ offsets,
+                  int* __restrict__ items, int* __restrict__ status) {
+    __shared__ int smem[kScanThreads / 64 + 1];
+    // E <= kMaxExperts = kScanThreads: one expert per thread.
+    const int e = threadIdx.x;
+    int cnt = 0;
+    if (e < E) {
+        int run = 0;
+        for (int c = 0; c < nchunks; ++c) {
+            const size_t i = (size_t)c * E + e;
+            const int h = chunk_hist[i];
+            chunk_hist[i] = run;  // exclusive prefix over chunks (uncapped rank base)
+            run += h;
+        }
+        cnt = min(run, cap);
+        counts[e] = cnt;
+    }
+    int slots = 0;
+    const int off = block_exclusive_scan(cnt, smem, &slots);
+    if (e < E) offsets[e] = off;
+    if (threadIdx.x == 0) offsets[E] = slots;
+    const int nm = (cnt + m_tile - 1) / m_tile;
+    int nitems = 0;
+    const int ioff = block_exclusive_scan(nm, smem, &nitems);
+    for (int j = 0; j < nm; ++j) {
+        const int it = ioff + j;
+        if (it < max_items) {
+            items[2 * it + 0] = e;
+            items[2 * it + 1] = j * m_tile;
+        }
+    }
+    if (threadIdx.x == 0) {
+        status[1] = min(nitems, max_items);
+        status[2] = slots;
+        if (nitems > max_items) atomicOr(&status[0], 1);
+    }
+}
+
+__global__ void __launch_bounds__(kRouteThreads)
+route_scatter_kernel(const int64_t* __restrict__ topk_idx, int P, int E, int nbits,
+                     const int* __restrict__ chunk_hist, const int* __restrict__ counts,
+                     const int* __restrict__ offsets, uint32_t* __restrict__ perm,
+                     int* __restrict__ pair_pos) {
+    constexpr int kWaves = kRouteThreads / 64;
+    __shared__ int run[kMaxExperts];
+    __shared__ int cntw[kWaves][kMaxExperts];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < E; i += blockDim.x) {
+        run[i] = chunk_hist[(size_t)blockIdx.x * E + i];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) cntw[w][i] = 0;
+    }
+    __syncthreads();
+    const int base = blockIdx.x * kRouteChunk;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int r0 = base; r0 < min(base + kRouteChunk, P); r0 += kRouteThreads) {
+        const int p = r0 + threadIdx.x;
+        const bool in = p < P;
+        const int64_t e64 = in ? topk_idx[p] : -1;
+        const bool ok = e64 >= 0 && e64 < E;
+        const int e = ok ? (int)e64 : 0;
+        // lanes holding the same expert id: AND of per-bit ballots
+        uint64_t m = __ballot(ok);
+        for (int b = 0; b < nbits; ++b) {
+            const uint64_t bb = __ballot(ok && ((e >> b) & 1));
+            m &= ((e >> b) & 1) ? bb : ~bb;
+        }
+        const int rank = __popcll(m & lt_mask);
+        const int wcnt = __popcll(m);
+        if (ok && rank == 0) cntw[wave][e] = wcnt;
+        __syncthreads();
+        if (ok) {
+            int pre = run[e];
+            for (int w = 0; w < wave; ++w) pre += cntw[w][e];
+            const int r = pre + rank;
+            if (r < counts[e]) {
+                const int pos = offsets[e] + r;
+                perm[pos] = (uint32_t)p;
+                pair_pos[p] = pos;
+            } else {
+                pair_pos[p] = -1;
+            }
+        } else if (in) {
+            pair_pos[p] = -1;
+        }
+        __syncthreads();
+        if (ok && rank == 0) {
+            atomicAdd(&run[e], wcnt);
+            cntw[wave][e] = 0;
+        }
+        __syncthreads();
+    }
+}
+
+// DISPATCH pool (diagnostic / parity): pool[slot][:] = x[perm[slot] / topk][:],
+// 16 bytes per thread.
+__global__ void __launch_bounds__(256)
+dispatch_gather_kernel(const uint8_t* __restrict__ x, int H, int topk,
+                       const uint32_t* __restrict__ perm, const int* __restrict__ status,
+                       uint8_t* __restrict__ pool) {
+    const int slot = blockIdx.x;
+    if (slot >= status[2]) return;
+    const size_t tok = perm[slot] / (uint32_t)topk;
+    const v4i* src = reinterpret_cast<const v4i*>(x + tok * H);
+    v4i* dst = reinterpret_cast<v4i*>(pool + (size_t)slot * H);
+    for (int c = threadIdx.x; c < H / 16; c += blockDim.x) dst[c] = src[c];
+}
+
+}  // namespace mm

@@ -1,0 +1,239 @@
+"""Shared GPU test plumbing: set up one MoE layer on the device through the
+public Python API, run it, and check it stage by stage against the oracle
+(the way check.cu checks the reference: routing exact, L1 fed with the device
+pool, L2 fed with the device ffn, REDUCE fed with the device L2 rows, then the
+whole chain end to end)."""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import torch
+
+import mini_mega_amd as mm
+from mini_mega_amd import inputs
+from oracle import oracle as orc
+
+# check.cu tolerances (test/check.cu:397-507, src/bench_check.cuh:583-596)
+L1_REL, L1_ABS = 7e-2, 2e-3
+L2_REL, L2_ABS = 1e-2, 1e-3
+RED_REL, RED_ABS = 1e-5, 1e-6
+# BASELINE end-to-end gate
+E2E_ABS_FRAC, E2E_COS = 2e-2, 0.9995
+
+
+@dataclasses.dataclass
+class Case:
+    E: int
+    K: int
+    H: int
+    I: int
+    T: int
+    x: np.ndarray            # [T, H] fp8 bytes
+    xsf: np.ndarray | None   # [T, H/128]
+    idx: np.ndarray          # [T, K] int64
+    wts: np.ndarray          # [T, K] float32
+    w1: torch.Tensor         # packed device weights
+    s1: torch.Tensor | None
+    w2: torch.Tensor
+    s2: torch.Tensor | None
+    win: int = 0
+    cap: int = 0
+
+    @property
+    def scaled(self):
+        return self.s1 is not None
+
+    @property
+    def G(self):
+        return mm.pairing_block(self.I)
+
+    def w1_logical(self, e: int) -> np.ndarray:
+        return inputs.unpack_tiles(self.w1[e].view(torch.uint8).cpu().numpy().ravel(),
+                                   2 * self.I, self.H)
+
+    def w2_logical(self, e: int) -> np.ndarray:
+        return inputs.unpack_tiles(self.w2[e].view(torch.uint8).cpu().numpy().ravel(),
+                                   self.H, self.I)
+
+    def s1_of(self, e):
+        return None if self.s1 is None else np.ascontiguousarray(self.s1[e].cpu().numpy())
+
+    def s2_of(self, e):
+        return None if self.s2 is None else np.ascontiguousarray(self.s2[e].cpu().numpy())
+
+
+def normal_case(E, K, H, I, T, seed, scaled=True, zipf=None, win=0, idx=None, wts=None):
+    _, xq, xsf = inputs.make_x(T, H, seed=seed, scaled=scaled)
+    (w1, s1), (w2, s2) = inputs.make_weights_normal(E, H, I, seed=seed + 100)
+    if idx is None:
+        idx, wts = inputs.route(T, E, K, seed=seed + 200, zipf_s=zipf)
+    torch.cuda.synchronize()
+    return Case(E, K, H, I, T, xq.cpu().numpy(), None if xsf is None else xsf.cpu().numpy(),
+                idx, wts, w1, s1 if scaled else None, w2, s2 if scaled else None, win=win)
+
+
+def checkcu_case(ranks, tpr, E=256, K=8, H=6144, I=2048, idx=None):
+    x, wts = orc.checkcu_inputs(ranks, tpr, H, K)
+    if idx is None:
+        idx = orc.balanced_routes(ranks, tpr, K, E // ranks)
+    w1, w2 = inputs.make_weights_checkcu(E, H, I)
+    torch.cuda.synchronize()
+    return Case(E, K, H, I, ranks * tpr, x, None, idx, wts, w1, None, w2, None)
+
+
+@dataclasses.dataclass
+class Run:
+    buf: object
+    y: np.ndarray        # bf16 output as float32 [T, H]
+    y32: np.ndarray      # fp32 output [T, H]
+    counts: np.ndarray
+    offsets: np.ndarray
+    perm: np.ndarray
+    pair_pos: np.ndarray
+    status: np.ndarray
+
+
+def run_layer(c: Case, skip_fetch_l2: bool = False) -> Run:
+    buf = mm.get_symm_buffer_for_mega_moe(None, c.E, c.T, c.K, c.H, c.I, expert_window=c.win)
+    buf.x.view(torch.uint8)[:c.T].copy_(torch.from_numpy(c.x))
+    if c.xsf is not None:
+        buf.x_sf[:c.T].copy_(torch.from_numpy(c.xsf))
+    buf.topk_idx[:c.T].copy_(torch.from_numpy(c.idx))
+    buf.topk_weights[:c.T].copy_(torch.from_numpy(c.wts))
+    y = torch.empty((c.T, c.H), dtype=torch.bfloat16, device="cuda")
+    l1 = (c.w1, c.s1) if c.scaled else c.w1
+    l2 = (c.w2, c.s2) if c.scaled else c.w2
+    mm.fp8_mega_moe(y, l1, l2, buf)
+    torch.cuda.synchronize()
+    offsets = buf.offsets().cpu().numpy()
+    slots = int(offsets[-1])
+    return Run(buf, y.float().cpu().numpy(), buf._y_fp32[:c.T].cpu().numpy(),
+               buf.counts().cpu().numpy(), offsets,
+               buf.perm(max(slots, 1)).cpu().numpy()[:slots].view(np.uint32),
+               buf.pair_pos(c.T).cpu().numpy().ravel(), buf.status().cpu().numpy())
+
+
+def check_routing(c: Case, r: Run):
+    counts, offsets, perm, pair_pos = orc.route(c.idx, c.E, c.cap if c.cap else None)
+    assert np.array_equal(r.counts, counts), "per-expert counts differ"
+    assert np.array_equal(r.offsets, offsets), "expert offsets differ"
+    assert np.array_equal(r.perm, perm), "canonical permutation differs"
+    assert np.array_equal(r.pair_pos, pair_pos), "pair slots differ"
+    assert r.status[0] == 0, f"device status word {r.status[0]}"
+
+
+def _bad(got, want, rel, abs_tol):
+    d = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    return d > np.maximum(abs_tol, rel * np.abs(want.astype(np.float64)))
+
+
+def slot_rows(c: Case, r: Run, e: int):
+    lo, hi = int(r.offsets[e]), int(r.offsets[e + 1])
+    toks = (r.perm[lo:hi] // c.K).astype(np.int64)
+    return lo, hi, toks
+
+
+def check_l1(c: Case, r: Run, e: int, max_rows: int = 64):
+    """Device ffn of expert e vs oracle ref_l1 on the same pool rows."""
+    lo, hi, toks = slot_rows(c, r, e)
+    hi = min(hi, lo + max_rows)
+    toks = toks[:hi - lo]
+    if hi == lo:
+        return
+    xs = np.ascontiguousarray(c.x[toks])
+    xsf = None if c.xsf is None else np.ascontiguousarray(c.xsf[toks])
+    want = orc.l1_rows(xs, xsf, c.w1_logical(e), c.s1_of(e), c.G)
+    ffn = r.buf.ffn(hi).cpu().numpy()[lo:hi]
+    table = orc.e4m3_decode_table()
+    got = table[ffn].astype(np.float64)
+    if c.scaled:
+        sf = r.buf.ffn_sf(hi).cpu().numpy()[lo:hi].astype(np.int32)
+        s = np.repeat(np.ldexp(1.0, sf - 127), 128, axis=1)
+        got = got * s
+        # the device scale must be the UE8M0 recipe applied to the device's own h
+        amax = np.abs(want).reshape(hi - lo, -1, 128).max(axis=2)
+        ref_sf = np.array([[orc.block_scale(a) for a in row] for row in amax])
+        assert np.all(np.abs(sf - ref_sf) <= 1), "ffn scale off by more than one binade"
+        abs_tol = L1_ABS * s
+    else:
+        abs_tol = L1_ABS
+        want = np.clip(want, -448.0, 448.0)
+    bad = _bad(got, want, L1_REL, abs_tol)
+    assert bad.sum() == 0, (f"L1 expert {e}: {bad.sum()} / {bad.size} outside tolerance; "
+                            f"max |d| {np.abs(got - want).max():.3e}")
+
+
+def check_l2(c: Case, r: Run, e: int, max_rows: int = 64):
+    """Device L2 rows of expert e vs oracle ref_l2 fed with the device ffn."""
+    lo, hi, _ = slot_rows(c, r, e)
+    hi = min(hi, lo + max_rows)
+    if hi == lo:
+        return
+    ffn = np.ascontiguousarray(r.buf.ffn(hi).cpu().numpy()[lo:hi])
+    fsf = np.ascontiguousarray(r.buf.ffn_sf(hi).cpu().numpy()[lo:hi]) if c.scaled else None
+    want = orc.l2_rows(ffn, fsf, c.w2_logical(e), c.s2_of(e))
+    l2 = r.buf.l2_out(hi).cpu().numpy()[lo:hi].view(np.uint16)
+    got = (l2.astype(np.uint32) << 16).view(np.float32)
+    scale = max(1.0, float(np.sqrt(np.mean(want.astype(np.float64) ** 2))))
+    bad = _bad(got, want, L2_REL, L2_ABS * scale)
+    assert bad.sum() == 0, (f"L2 expert {e}: {bad.sum()} / {bad.size} outside tolerance; "
+                            f"max |d| {np.abs(got - want).max():.3e}")
+
+
+def check_reduce(c: Case, r: Run):
+    """Device y (fp32) vs oracle ref_reduce fed with the device L2 rows: same
+    bf16 inputs, same k order, product-then-add -> bit-exact."""
+    slots = int(r.offsets[-1])
+    l2 = np.ascontiguousarray(r.buf.l2_out(max(slots, 1)).cpu().numpy().view(np.uint16))
+    y, yb = orc.reduce(l2, r.pair_pos.reshape(c.T, c.K), c.wts, c.T, c.K)
+    bad = _bad(r.y32, y, RED_REL, RED_ABS)
+    assert bad.sum() == 0, f"REDUCE: {bad.sum()} outside 1e-5/1e-6"
+    assert np.array_equal(r.y32.view(np.uint32), y.view(np.uint32)), "REDUCE not bit-exact"
+    assert np.array_equal(r.y.astype(np.float32), ((yb.astype(np.uint32) << 16)
+                                                   .view(np.float32))), "bf16 y differs"
+
+
+def e2e_metrics(got: np.ndarray, want: np.ndarray):
+    got = got.astype(np.float64)
+    want = want.astype(np.float64)
+    rms = float(np.sqrt(np.mean(want ** 2)))
+    err = float(np.abs(got - want).max())
+    cos = float((got * want).sum() / (np.linalg.norm(got) * np.linalg.norm(want) + 1e-300))
+    return err, rms, cos
+
+
+def check_e2e(c: Case, r: Run, nthreads: int = 16):
+    """Whole chain vs the oracle's own chain (no device intermediates)."""
+    w1 = np.stack([c.w1_logical(e) for e in range(c.E)])
+    w2 = np.stack([c.w2_logical(e) for e in range(c.E)])
+    s1 = None if c.s1 is None else np.ascontiguousarray(c.s1.cpu().numpy())
+    s2 = None if c.s2 is None else np.ascontiguousarray(c.s2.cpu().numpy())
+    ref = orc.layer(c.x, c.xsf, w1, s1, w2, s2, c.idx, c.wts, E=c.E, G=c.G, scaled=c.scaled,
+                    nthreads=nthreads, cap=c.cap if c.cap else None)
+    err, rms, cos = e2e_metrics(r.y, ref["y"])
+    assert err <= E2E_ABS_FRAC * rms and cos >= E2E_COS, (
+        f"end-to-end: max_abs {err:.3e} rms {rms:.3e} cos {cos:.6f}")
+    return err, rms, cos
+
+
+def check_e2e_tokens(c: Case, r: Run, tokens, nthreads: int = 16):
+    """End-to-end on a subset of tokens at full size: the oracle runs the sub
+    problem restricted to those tokens and the experts they use (relabelled)."""
+    tokens = np.asarray(tokens)
+    sub_idx = c.idx[tokens]
+    experts = np.unique(sub_idx[(sub_idx >= 0) & (sub_idx < c.E)])
+    remap = {int(e): i for i, e in enumerate(experts)}
+    idx2 = np.vectorize(lambda v: remap.get(int(v), -1))(sub_idx).astype(np.int64)
+    w1 = np.stack([c.w1_logical(int(e)) for e in experts])
+    w2 = np.stack([c.w2_logical(int(e)) for e in experts])
+    s1 = None if c.s1 is None else np.ascontiguousarray(c.s1[torch.from_numpy(experts)].cpu().numpy())
+    s2 = None if c.s2 is None else np.ascontiguousarray(c.s2[torch.from_numpy(experts)].cpu().numpy())
+    xs = np.ascontiguousarray(c.x[tokens])
+    xsf = None if c.xsf is None else np.ascontiguousarray(c.xsf[tokens])
+    ref = orc.layer(xs, xsf, w1, s1, w2, s2, idx2, np.ascontiguousarray(c.wts[tokens]),
+                    E=len(experts), G=c.G, scaled=c.scaled, nthreads=nthreads)
+    err, rms, cos = e2e_metrics(r.y[tokens], ref["y"])
+    assert err <= E2E_ABS_FRAC * rms and cos >= E2E_COS, (
+        f"end-to-end (token subset): max_abs {err:.3e} rms {rms:.3e} cos {cos:.6f}")
+    return err, rms, cos

@@ -1,0 +1,104 @@
+"""CPU tests of the C-ABI boundary: the library loads without a GPU, exports
+every extern "C" symbol declared in include/megakernel.h, the ctypes mirror of
+MegaLaunchArgs matches the C struct, the workspace layout is sane, and bad
+shapes are rejected.  No compute is launched here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import mini_mega_amd as mm
+from mini_mega_amd import _lib
+from mini_mega_amd.inputs import paired_to_torch_rows, unpack_tiles
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_c_symbols():
+    text = open(os.path.join(ROOT, "include", "megakernel.h")).read()
+    block = text[text.index('extern "C" {'):]
+    return sorted(set(re.findall(r"\b(mm_[a-z_0-9]+)\s*\(", block)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = mm.lib()
+    syms = _declared_c_symbols()
+    assert len(syms) >= 18
+    for s in syms:
+        assert hasattr(L, s), f"{s} not exported"
+    assert set(syms) == set(_lib.EXPORTS)
+
+
+def test_args_mirror_matches_c_struct():
+    L = mm.lib()
+    assert L.mm_abi_version() == 1
+    assert L.mm_args_size() == ctypes.sizeof(mm.MegaLaunchArgs)
+    for name, *_ in mm.MegaLaunchArgs._fields_:
+        assert L.mm_args_offset(name.encode()) == getattr(mm.MegaLaunchArgs, name).offset
+    assert L.mm_args_offset(b"no_such_field") == -1
+
+
+@pytest.mark.parametrize("T", [32, 512, 2048, 8192])
+def test_layout_regions_aligned_and_disjoint(T):
+    E, K, H, I = 256, 8, 6144, 2048
+    L = mm.layout(T, K, E, H, I)
+    names = ["status", "chunk_hist", "counts", "offsets", "items", "perm", "pair_pos", "xq",
+             "xq_sf", "ffn", "ffn_sf", "l2", "total"]
+    offs = [getattr(L, n) for n in names]
+    assert all(o % 256 == 0 for o in offs)
+    assert offs == sorted(offs)
+    P = T * K
+    assert L.l2 + P * H * 2 <= L.total
+    assert L.ffn_sf - L.ffn >= P * I
+    assert L.max_items >= (P + L.m_tile - 1) // L.m_tile + E - 1
+
+
+@pytest.mark.parametrize("dims", [(32, 8, 256, 100, 2048), (32, 8, 256, 6144, 200),
+                                  (32, 0, 256, 6144, 2048), (32, 8, 2000, 6144, 2048),
+                                  (0, 8, 256, 6144, 2048)])
+def test_layout_rejects_bad_dims(dims):
+    with pytest.raises(mm.MegaError):
+        mm.layout(*dims)
+
+
+def test_launch_rejects_null_workspace_without_touching_gpu():
+    L = mm.lib()
+    a = mm.MegaLaunchArgs(tokens=4, max_tokens=4)
+    assert L.mm_launch_full(ctypes.byref(a), None) == 1  # kErrNullPointer
+    a = mm.MegaLaunchArgs(tokens=8, max_tokens=4, rwk=1, self=1, topk_idx=1, w1=1, w2=1)
+    assert L.mm_launch_full(ctypes.byref(a), None) == 4  # kErrTooManyTokens
+    a = mm.MegaLaunchArgs(tokens=4, max_tokens=4, rwk=1, self=1, topk_idx=1, w1=1, w2=1,
+                          workspace_bytes=16)
+    assert L.mm_launch_full(ctypes.byref(a), None) == 3  # kErrWorkspace
+
+
+def _pack_numpy(w):
+    """Tile layout written from the byte formula in mm_device.h (tile_byte)."""
+    n, k = w.shape
+    out = np.zeros(n * k, np.uint8)
+    r = np.arange(n)[:, None]
+    c = np.arange(k)[None, :]
+    nt, kt, rr, kk = r // 16, c // 128, r % 16, c % 128
+    off = (nt * (k // 128) + kt) * 2048 + ((kk % 32) // 16) * 1024 + (rr + 16 * (kk // 32)) * 16 \
+        + kk % 16
+    out[off.ravel()] = w.ravel()
+    return out
+
+
+def test_unpack_inverts_tile_formula():
+    w = np.random.default_rng(0).integers(0, 256, size=(64, 384)).astype(np.uint8)
+    assert np.array_equal(unpack_tiles(_pack_numpy(w), 64, 384), w)
+
+
+@pytest.mark.parametrize("I", [128, 2048])
+def test_paired_row_map_is_reference_pairing(I):
+    """Paired row rho (gate of h at (h/G)*2G + h%G, up at +G; src/bench_check.cuh:
+    444-445) maps to torch row h (gate) or I + h (up)."""
+    G = mm.pairing_block(I)
+    m = paired_to_torch_rows(I)
+    assert sorted(m.tolist()) == list(range(2 * I))
+    for h in sorted({0, 1, G - 1, min(G, I - 1), I - 1}):
+        assert m[(h // G) * 2 * G + h % G] == h
+        assert m[(h // G) * 2 * G + h % G + G] == I + h

@@ -1,0 +1,298 @@
+"""GPU parity tests: the HIP layer (through the C ABI) against the oracle.
+
+Bars: routing / permutation / counts / byte work bit-exact; L1, L2, REDUCE at
+check.cu's staged tolerances; the whole layer at max|d| <= 2e-2 rms(y) and
+cos >= 0.9995.
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import mini_mega_amd as mm
+from mini_mega_amd import inputs
+from oracle import oracle as orc
+
+import moe_case as mc
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    torch.cuda.set_device(0)
+    mm.lib()
+    yield
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+# --------------------------------------------------------- device codecs --
+def test_device_fp8_and_bf16_conversion_bit_exact():
+    _say("convert selftest")
+    t = orc.e4m3_decode_table()
+    fin = np.sort(np.unique(t[np.isfinite(t)]))
+    mids = (fin[1:] + fin[:-1]) / 2
+    rng = np.random.default_rng(3)
+    v = np.concatenate([fin, mids, np.nextafter(mids.astype(np.float32), np.float32(1e9)),
+                        np.nextafter(mids.astype(np.float32), np.float32(-1e9)),
+                        rng.standard_normal(20000) * 30, rng.standard_normal(5000) * 0.01,
+                        [448.0, 464.0, 500.0, 1e6, -1e6, 0.0, -0.0]]).astype(np.float32)
+    src = torch.from_numpy(v).cuda()
+    o8 = torch.empty(v.size, dtype=torch.uint8, device="cuda")
+    o16 = torch.empty(v.size, dtype=torch.int16, device="cuda")
+    assert mm.lib().mm_selftest_convert(src.data_ptr(), v.size, o8.data_ptr(), o16.data_ptr(),
+                                        _stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(o8.cpu().numpy(), orc.e4m3_quantize(v))
+    assert np.array_equal(o16.cpu().numpy().view(np.uint16), orc.f32_to_bf16(v))
+
+
+def test_pack_weights_roundtrip():
+    _say("pack roundtrip")
+    rng = np.random.default_rng(4)
+    w = rng.integers(0, 256, size=(3, 64, 384)).astype(np.uint8)
+    packed = mm.pack_weights(torch.from_numpy(w).cuda().view(torch.float8_e4m3fn))
+    torch.cuda.synchronize()
+    p = packed.view(torch.uint8).cpu().numpy()
+    for e in range(3):
+        assert np.array_equal(inputs.unpack_tiles(p[e].ravel(), 64, 384), w[e])
+
+
+def test_fill_weights_lane_matches_wprobe():
+    _say("fill_weights_lane")
+    n, k = 512, 768
+    w = torch.empty(n * k, dtype=torch.uint8, device="cuda")
+    assert mm.lib().mm_fill_weights_lane(w.data_ptr(), n, k, 17, _stream()) == 0
+    torch.cuda.synchronize()
+    got = inputs.unpack_tiles(w.cpu().numpy(), n, k)
+    assert np.array_equal(got, orc.wprobe_matrix(17, 0, n, k))
+
+
+@pytest.mark.parametrize("scaled", [True, False])
+def test_quant_act_matches_oracle(scaled):
+    _say(f"quant_act scaled={scaled}")
+    xb, q, sf = inputs.make_x(64, 1024, seed=9, scaled=scaled)
+    torch.cuda.synchronize()
+    x32 = xb.float().cpu().numpy()
+    if scaled:
+        rq, rsf = orc.quant_rows_ue8m0(x32)
+        assert np.array_equal(sf.cpu().numpy(), rsf)
+    else:
+        rq = orc.e4m3_quantize(x32).reshape(x32.shape)
+    assert np.array_equal(q.cpu().numpy(), rq)
+
+
+def test_weight_generator_scales_follow_recipe():
+    _say("fill_weights_normal")
+    (w1, s1), _ = inputs.make_weights_normal(2, 256, 128, seed=5)
+    torch.cuda.synchronize()
+    t = orc.e4m3_decode_table()
+    wl = inputs.unpack_tiles(w1[1].view(torch.uint8).cpu().numpy().ravel(), 256, 256)
+    s = s1[1].cpu().numpy().astype(np.int32)
+    deq = t[wl].reshape(2, 128, 2, 128) * np.ldexp(1.0, s - 127)[:, None, :, None]
+    amax_q = np.abs(t[wl]).reshape(2, 128, 2, 128).max(axis=(1, 3))
+    assert np.all(amax_q <= 448) and np.all(amax_q >= 192)  # amax/sf in (224, 448] before RNE
+    assert 0.015 < deq.std() < 0.025
+
+
+# ----------------------------------------------------------------- routing --
+def _route_only(E, K, H, I, idx, cap=0):
+    T = idx.shape[0]
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, max(T, 1), K, H, I)
+    if T:
+        buf.topk_idx[:T].copy_(torch.from_numpy(idx))
+    a = buf.make_args(T, buf.x, buf.x, slot_capacity=cap)  # weights unused by the prelude
+    assert mm.lib().mm_launch_prelude(ctypes.byref(a), _stream()) == 0
+    torch.cuda.synchronize()
+    off = buf.offsets().cpu().numpy()
+    slots = int(off[-1])
+    return (buf.counts().cpu().numpy(), off,
+            buf.perm(max(slots, 1)).cpu().numpy()[:slots].view(np.uint32),
+            buf.pair_pos(max(T, 1)).cpu().numpy().ravel()[:T * K], buf.status().cpu().numpy())
+
+
+def _check_route(E, K, idx, cap=0, H=256, I=128):
+    counts, off, perm, pos, status = _route_only(E, K, H, I, idx, cap)
+    rc, ro, rp, rpos = orc.route(idx, E, cap if cap else None)
+    assert status[0] == 0
+    assert np.array_equal(counts, rc)
+    assert np.array_equal(off, ro)
+    assert np.array_equal(perm, rp)
+    assert np.array_equal(pos, rpos)
+
+
+@pytest.mark.parametrize("T,K,E", [(32, 2, 8), (512, 8, 256), (2048, 8, 256), (8192, 8, 256),
+                                   (1, 8, 256), (300, 6, 64), (1000, 8, 1024)])
+def test_routing_bit_exact(T, K, E):
+    _say(f"routing T={T} K={K} E={E}")
+    idx, _ = inputs.route(T, E, K, seed=T + E)
+    _check_route(E, K, idx)
+
+
+def test_routing_invalid_ids_and_cap():
+    _say("routing invalid ids + cap")
+    rng = np.random.default_rng(7)
+    idx = rng.integers(-3, 70, size=(700, 8)).astype(np.int64)  # E=64: ids 64..69 invalid
+    _check_route(64, 8, idx)
+    _check_route(64, 8, idx, cap=40)
+    _check_route(64, 8, np.full((100, 8), 3, np.int64))  # one hot expert, duplicates
+
+
+@pytest.mark.parametrize("launch", [804900, 809200, 853000])
+def test_routing_tk_fixtures(launch):
+    _say(f"routing TK launch {launch}")
+    from test_oracle import _tk_launches
+    per_expert = _tk_launches()[launch]
+    idx = orc.routes_from_counts(per_expert, 32, 8, int(per_expert.sum()) // 256, 8)
+    counts, *_ = _route_only(256, 8, 6144, 2048, idx)
+    assert np.array_equal(counts, per_expert)
+    _check_route(256, 8, idx, H=6144, I=2048)
+
+
+def test_routing_skewed_zipf():
+    _say("routing zipf")
+    idx, _ = inputs.route(2048, 256, 8, seed=11, zipf_s=1.1)
+    _check_route(256, 8, idx, H=6144, I=2048)
+
+
+def test_dispatch_pool_is_gathered_rows():
+    _say("dispatch pool")
+    E, K, H, I, T = 16, 4, 512, 128, 100
+    c = mc.normal_case(E, K, H, I, T, seed=21, scaled=False)
+    r = mc.run_layer(c)
+    slots = int(r.offsets[-1])
+    pool = torch.empty((slots, H), dtype=torch.uint8, device="cuda")
+    a = r.buf.make_args(T, c.w1, c.w2)
+    assert mm.lib().mm_launch_dispatch(ctypes.byref(a), pool.data_ptr(), _stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.cpu().numpy(), c.x[r.perm // K])
+
+
+# ------------------------------------------------------------- the layer --
+SMALL = [
+    # E, K, H, I, T, scaled, win
+    (8, 2, 256, 128, 32, True, 0),      # BASELINE config 0 (smoke)
+    (8, 2, 256, 128, 32, False, 0),
+    (32, 8, 1024, 512, 200, True, 0),
+    (32, 8, 1024, 512, 200, False, 16),
+    (16, 4, 512, 256, 300, True, 64),
+    (64, 8, 512, 256, 96, True, 32),
+]
+
+
+@pytest.mark.parametrize("E,K,H,I,T,scaled,win", SMALL)
+def test_layer_staged_and_e2e(E, K, H, I, T, scaled, win):
+    _say(f"layer E={E} K={K} H={H} I={I} T={T} scaled={scaled} win={win}")
+    c = mc.normal_case(E, K, H, I, T, seed=E + T, scaled=scaled, win=win)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    busiest = int(np.argmax(r.counts))
+    for e in sorted({busiest, int(np.argmin(np.where(r.counts > 0, r.counts, 1 << 30)))}):
+        mc.check_l1(c, r, e)
+        mc.check_l2(c, r, e)
+    mc.check_reduce(c, r)
+    err, rms, cos = mc.check_e2e(c, r)
+    _say(f"  e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
+def test_layer_bf16_input_fold():
+    """bf16xfp8: x arrives as bf16 and is folded to fp8 inside the layer
+    (reference x_fold_body, src/prologue.cuh:103-122)."""
+    _say("bf16 input fold")
+    E, K, H, I, T = 16, 4, 512, 256, 64
+    xb, xq, xsf = inputs.make_x(T, H, seed=5, scaled=True)
+    (w1, s1), (w2, s2) = inputs.make_weights_normal(E, H, I, seed=6)
+    idx, wts = inputs.route(T, E, K, seed=7)
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I, mma_type="bf16xfp8")
+    buf.x[:T].copy_(xb)
+    buf.topk_idx[:T].copy_(torch.from_numpy(idx))
+    buf.topk_weights[:T].copy_(torch.from_numpy(wts))
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    mm.bf16_fp8_mega_moe(y, (w1, s1), (w2, s2), buf)
+    torch.cuda.synchronize()
+    c = mc.Case(E, K, H, I, T, xq.cpu().numpy(), xsf.cpu().numpy(), idx, wts, w1, s1, w2, s2)
+    r = mc.Run(buf, y.float().cpu().numpy(), buf._y_fp32[:T].cpu().numpy(),
+               buf.counts().cpu().numpy(), buf.offsets().cpu().numpy(), None, None, None)
+    mc.check_e2e(c, r)
+
+
+# -------------------------------------------------- check.cu-identical inputs --
+def test_checkcu_inputs_full_size_t512():
+    """check.cu's own inputs at R=32, TPR=16 (T=512) remapped to one GPU:
+    routing exact, every ffn byte saturated to 0x7E (closed form), L2 and
+    REDUCE at check.cu tolerances."""
+    _say("check.cu inputs T=512 full size")
+    c = mc.checkcu_case(32, 16)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    slots = int(r.offsets[-1])
+    ffn = r.buf.ffn(slots).cpu().numpy()
+    assert np.all(ffn == 0x7E)
+    for e in (0, 7, 255):
+        mc.check_l2(c, r, e)
+    mc.check_reduce(c, r)
+
+
+# ------------------------------------------------------------ full sizes --
+@pytest.mark.parametrize("T,zipf", [(512, None), (2048, None), (2048, 1.1)])
+def test_full_size_layer(T, zipf):
+    """BASELINE configs 1, 2, 4 at full size: routing exact, staged L1/L2 on
+    the busiest / a median / the lightest expert, REDUCE bit-exact, and the
+    whole chain on a token subset."""
+    _say(f"full size T={T} zipf={zipf}")
+    c = mc.normal_case(256, 8, 6144, 2048, T, seed=T + 1, scaled=True, zipf=zipf)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    nz = np.nonzero(r.counts)[0]
+    order = nz[np.argsort(r.counts[nz], kind="stable")]
+    for e in {int(order[-1]), int(order[len(order) // 2]), int(order[0])}:
+        mc.check_l1(c, r, e, max_rows=48)
+        mc.check_l2(c, r, e, max_rows=48)
+    mc.check_reduce(c, r)
+    err, rms, cos = mc.check_e2e_tokens(c, r, [0, 1, T // 2, T - 1])
+    _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
+def test_graph_replay_matches_eager():
+    """N launches captured in one HIP graph, replayed three times with eager
+    work in between; every replay must reproduce the eager output bit for bit
+    (reference run_graph, test/check.cu:533-745)."""
+    _say("graph replay")
+    E, K, H, I, T = 32, 8, 1024, 512, 128
+    c = mc.normal_case(E, K, H, I, T, seed=3, scaled=True)
+    r = mc.run_layer(c)
+    buf = r.buf
+    ys = [torch.empty((T, H), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for y in ys:
+                mm.fp8_mega_moe(y, (c.w1, c.s1), (c.w2, c.s2), buf)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(3):
+        for y in ys:
+            y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for y in ys:
+            assert np.array_equal(y.float().cpu().numpy(), r.y), f"replay {rep} differs"
+        # eager launch between replays must not disturb the graph's result
+        y2 = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        mm.fp8_mega_moe(y2, (c.w1, c.s1), (c.w2, c.s2), buf)
+        torch.cuda.synchronize()
+        assert np.array_equal(y2.float().cpu().numpy(), r.y)

@@ -1,0 +1,298 @@
+"""CPU tests that pin the oracle (oracle/moe_oracle.c) before it is trusted.
+
+Each check compares against something independent of the oracle's own code:
+torch's float8_e4m3fn / bfloat16 casts, closed forms, brute force on tiny
+inputs, fp64 GEMMs, the reference's TK_INFO fixtures, or invariants a wrong
+term / sign / index / transposition would break.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+rng = np.random.default_rng(1234)
+
+
+# ------------------------------------------------------------------ codecs --
+def test_e4m3_decode_matches_torch_all_256():
+    table = orc.e4m3_decode_table()
+    ref = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float()
+    ref = ref.numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(table), nan)
+    assert nan.sum() == 2  # 0x7F / 0xFF
+    assert np.array_equal(table[~nan], ref[~nan])
+    assert table[0x7E] == 448.0 and table[0x01] == 2.0 ** -9 and table[0x80] == 0.0
+
+
+def _edge_values():
+    t = orc.e4m3_decode_table()
+    fin = t[np.isfinite(t)]
+    mids = []
+    s = np.sort(np.unique(fin))
+    mids = (s[1:] + s[:-1]) / 2  # exact ties
+    nudge = np.concatenate([np.nextafter(mids.astype(np.float32), np.float32(np.inf)),
+                            np.nextafter(mids.astype(np.float32), np.float32(-np.inf))])
+    rand = rng.standard_normal(4000).astype(np.float32) * np.float32(50.0)
+    small = rng.standard_normal(2000).astype(np.float32) * np.float32(0.01)
+    return np.concatenate([fin, mids, nudge, rand, small, [0.0, -0.0, 447.9, 448.0]]).astype(
+        np.float32)
+
+
+def test_e4m3_quantize_matches_torch_rne_on_clamped_values():
+    v = _edge_values()
+    got = orc.e4m3_quantize(v)
+    ref = torch.from_numpy(np.clip(v, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert np.array_equal(got, ref.numpy())
+
+
+def test_e4m3_quantize_saturates_and_nan():
+    got = orc.e4m3_quantize(np.array([448.0, 464.0, 480.0, 1e9, np.inf, -1e9, -np.inf],
+                                     np.float32))
+    assert list(got) == [0x7E, 0x7E, 0x7E, 0x7E, 0x7E, 0xFE, 0xFE]
+    assert orc.e4m3_quantize(np.array([np.nan], np.float32))[0] == 0x7F
+
+
+def test_bf16_rne_matches_torch():
+    v = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 1000,
+                        np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8, 3.4e38,
+                                  np.inf, -np.inf, 1e-40], np.float32)]).astype(np.float32)
+    got = orc.f32_to_bf16(v)
+    ref = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------- UE8M0 --
+def test_ceil_ue8m0_closed_form():
+    for e in range(-20, 20):
+        assert orc.ceil_ue8m0(2.0 ** e) == 127 + e          # exact powers map to themselves
+        assert orc.ceil_ue8m0(2.0 ** e * 1.0001) == 128 + e  # anything above rounds up
+        assert orc.ceil_ue8m0(2.0 ** e * 0.9999) == 127 + e
+
+
+@pytest.mark.parametrize("scale", [1e-3, 1.0, 37.0, 1e4])
+def test_quant_rows_ue8m0_invariants(scale):
+    x = (rng.standard_normal((16, 512)) * scale).astype(np.float32)
+    q, sf = orc.quant_rows_ue8m0(x)
+    table = orc.e4m3_decode_table()
+    s = np.ldexp(1.0, sf.astype(np.int32) - 127)
+    amax = np.abs(x).reshape(16, 4, 128).max(axis=2)
+    # ceil-to-power-of-two of amax/448: amax/s in (224, 448]
+    assert np.all(amax / s <= 448.0) and np.all(amax / s > 224.0)
+    deq = table[q].reshape(16, 4, 128) * s[:, :, None]
+    err = np.abs(deq - x.reshape(16, 4, 128))
+    # e4m3 half-ulp: 2^-4 relative for normals, 2^-10 * s absolute for subnormals
+    assert np.all(err <= np.maximum(np.abs(x.reshape(16, 4, 128)) * 2.0 ** -4,
+                                    s[:, :, None] * 2.0 ** -10) + 1e-30)
+
+
+def test_quant_blocks_ue8m0_scale_per_block():
+    w = (rng.standard_normal((256, 384)) * 0.02).astype(np.float32)
+    w[:128, :128] *= 100.0  # one hot block: its scale must differ from its neighbours'
+    q, sf = orc.quant_blocks_ue8m0(w)
+    assert sf.shape == (2, 3)
+    assert sf[0, 0] > sf[0, 1] and sf[0, 0] > sf[1, 0]
+    amax = np.abs(w.reshape(2, 128, 3, 128)).max(axis=(1, 3))
+    s = np.ldexp(1.0, sf.astype(np.int32) - 127)
+    assert np.all(amax / s <= 448.0) and np.all(amax / s > 224.0)
+
+
+# ----------------------------------------------------------------- routing --
+def _route_bruteforce(idx, E, cap):
+    T, K = idx.shape
+    flat = idx.ravel()
+    pos = np.full(flat.size, -1, np.int64)
+    perm, counts = [], np.zeros(E, np.int64)
+    for e in range(E):
+        members = [p for p in range(flat.size) if flat[p] == e][:cap]
+        counts[e] = len(members)
+        for p in members:
+            pos[p] = len(perm)
+            perm.append(p)
+    return counts, np.array(perm, np.int64), pos
+
+
+@pytest.mark.parametrize("T,K,E,cap", [(7, 3, 5, 100), (33, 4, 16, 100), (40, 8, 16, 9),
+                                       (1, 1, 1, 100)])
+def test_route_matches_bruteforce(T, K, E, cap):
+    idx = rng.integers(-2, E + 2, size=(T, K)).astype(np.int64)  # includes invalid ids
+    counts, offsets, perm, pair_pos = orc.route(idx, E, cap)
+    bc, bperm, bpos = _route_bruteforce(idx, E, cap)
+    assert np.array_equal(counts, bc)
+    assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(bc)]))
+    assert np.array_equal(perm, bperm)
+    assert np.array_equal(pair_pos, bpos)
+
+
+def _tk_launches():
+    import os
+    import re
+    path = os.path.join(os.path.dirname(__file__), "golden", "tk_info_anchors.log")
+    data = {}
+    for line in open(path):
+        m = re.search(r"\[TK_INFO\] rank=(\d+) launch=(\d+) n=8 : (.*)", line)
+        data.setdefault(int(m.group(2)), {})[int(m.group(1))] = list(map(int, m.group(3).split()))
+    out = {}
+    for launch, ranks in data.items():
+        assert len(ranks) == 32
+        out[launch] = np.array([ranks[r] for r in range(32)], np.int32).ravel()
+    return out
+
+
+@pytest.mark.parametrize("launch", [804900, 809200, 853000])
+def test_tk_fixture_routes_reproduce_counts(launch):
+    """test/mega_common.cuh:460-482 + route_count_deviation (:485-495): routes
+    rebuilt from a TK_INFO launch hit the logged per-expert counts exactly."""
+    per_expert = _tk_launches()[launch]
+    total = int(per_expert.sum())
+    assert total % (32 * 8) == 0
+    tokens = total // (32 * 8)
+    idx = orc.routes_from_counts(per_expert, 32, 8, tokens, 8)
+    counts, offsets, perm, pair_pos = orc.route(idx, 256)
+    assert np.array_equal(counts, per_expert)
+    for row in idx:
+        assert len(set(row.tolist())) == 8  # duplicate free per token
+
+
+def test_balanced_routes_exactly_16_per_expert():
+    """make_routes(Balanced) (src/bench_check.cuh:52-55): every expert gets
+    exactly TPR*R*8/E pairs at TPR 16, R 32."""
+    idx = orc.balanced_routes(32, 16, 8, 8)
+    counts, *_ = orc.route(idx, 256)
+    assert np.all(counts == 16)
+
+
+# ---------------------------------------------------------------- L1 / L2 --
+def _rand_fp8(shape, scale):
+    v = (rng.standard_normal(shape) * scale).astype(np.float32)
+    return orc.e4m3_quantize(np.clip(v, -448, 448)).reshape(shape)
+
+
+def test_l1_matches_fp64_gemm_and_pairing():
+    H, I, G, rows = 256, 256, 256, 5
+    x = _rand_fp8((rows, H), 1.0)
+    w = _rand_fp8((2 * I, H), 0.05)
+    t = orc.e4m3_decode_table().astype(np.float64)
+    xd, wd = t[x], t[w]
+    h_idx = np.arange(I)
+    grow = (h_idx // G) * 2 * G + h_idx % G
+    g = xd @ wd[grow].T
+    u = xd @ wd[grow + G].T
+    want = g / (1 + np.exp(-g)) * u
+    got = orc.l1_rows(x, None, w, None, G)
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-4)
+    # gate/up swapped would give silu(u)*g: must be far from the oracle
+    swapped = u / (1 + np.exp(-u)) * g
+    assert not np.allclose(got, swapped, rtol=1e-2, atol=1e-2)
+
+
+def test_l1_pairing_block_128():
+    """I = 128 uses pairing block G = 128: gate rows 0..127, up rows 128..255."""
+    H, I, G = 256, 128, 128
+    x = _rand_fp8((3, H), 1.0)
+    w = np.zeros((2 * I, H), np.uint8)
+    w[5, :] = 0x38  # 1.0 on gate row of h=5
+    w[128 + 5, :] = 0x40  # 2.0 on up row of h=5
+    got = orc.l1_rows(x, None, w, None, G)
+    t = orc.e4m3_decode_table().astype(np.float64)
+    g = t[x].sum(axis=1)
+    want = g / (1 + np.exp(-g)) * (2 * g)
+    assert np.allclose(got[:, 5], want, rtol=1e-5)
+    assert np.all(got[:, np.arange(I) != 5] == 0)
+
+
+def test_scaled_with_unit_scales_equals_unscaled_bitwise():
+    H, I, G, rows = 256, 128, 128, 4
+    x = _rand_fp8((rows, H), 1.0)
+    w1 = _rand_fp8((2 * I, H), 0.05)
+    w2 = _rand_fp8((H, I), 0.05)
+    one_x = np.full((rows, H // 128), 127, np.uint8)
+    one_w1 = np.full((2 * I // 128, H // 128), 127, np.uint8)
+    one_w2 = np.full((H // 128, I // 128), 127, np.uint8)
+    a = orc.l1_rows(x, None, w1, None, G)
+    b = orc.l1_rows(x, one_x, w1, one_w1, G)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    f = orc.quant_ffn(a, False)[0]
+    one_f = np.full((rows, I // 128), 127, np.uint8)
+    assert np.array_equal(orc.l2_rows(f, None, w2, None).view(np.uint32),
+                          orc.l2_rows(f, one_f, w2, one_w2).view(np.uint32))
+
+
+def test_l2_scale_is_exact_power_of_two_linearity():
+    H, I, rows = 256, 256, 3
+    f = _rand_fp8((rows, I), 1.0)
+    w2 = _rand_fp8((H, I), 0.05)
+    s = np.full((H // 128, I // 128), 127, np.uint8)
+    base = orc.l2_rows(f, None, w2, s)
+    s2 = s.copy()
+    s2[1, :] += 3  # output rows 128..255 scaled by 8 exactly
+    scaled = orc.l2_rows(f, None, w2, s2)
+    assert np.array_equal(scaled[:, :128], base[:, :128])
+    assert np.array_equal(scaled[:, 128:], base[:, 128:] * 8)
+    t = orc.e4m3_decode_table().astype(np.float64)
+    assert np.allclose(base, t[f] @ t[w2].T, rtol=1e-4, atol=1e-4)
+
+
+def test_reduce_order_and_invalid_pairs():
+    T, K, H = 4, 3, 256
+    l2 = orc.f32_to_bf16(rng.standard_normal(6 * H).astype(np.float32)).reshape(6, H)
+    pair_pos = np.array([[0, 1, -1], [2, -1, 3], [-1, -1, -1], [4, 5, 0]], np.int32)
+    w = rng.random((T, K)).astype(np.float32)
+    y, yb = orc.reduce(l2, pair_pos, w, T, K)
+    vals = np.array([orc.lib().orc_bf16_to_f32(int(b)) for b in l2.ravel()],
+                    np.float32).reshape(6, H)
+    for t in range(T):
+        acc = np.zeros(H, np.float32)
+        for k in range(K):
+            if pair_pos[t, k] >= 0:
+                acc = (acc + (vals[pair_pos[t, k]] * w[t, k]).astype(np.float32)).astype(np.float32)
+        assert np.array_equal(y[t], acc)
+    assert np.all(y[2] == 0)
+
+
+# ------------------------------------------------------- check.cu closed form --
+def test_checkcu_inputs_saturate_every_ffn_byte():
+    """check.cu inputs are all-positive with g, u ~ 4e5..9e5, so every L1
+    output saturates to 448 = 0x7E; and g == u because 131*256 = 0 mod 64."""
+    H, I, G = 6144, 2048, 256
+    x, w = orc.checkcu_inputs(2, 2, H, 8)
+    w1e = orc.wprobe_matrix(17, 0, 2 * I, H)
+    assert np.array_equal(w1e[:256], w1e[256:512])  # gate rows == up rows (period 64)
+    h = orc.l1_rows(x[:2], None, w1e, None, G)[:, :64]
+    assert np.all(h > 448.0)
+    q, _ = orc.quant_ffn(np.ascontiguousarray(h), False)
+    assert np.all(q == 0x7E)
+    assert np.allclose(w[0], 1.0 + 0.01 * (np.arange(8) % 7))
+
+
+def test_layer_chain_small_against_fp64_model():
+    """Full chain on a tiny layer vs a float64 numpy restatement of
+    torch/tests/test_fp8_mega_moe.py:28-48 (reference())."""
+    E, K, H, I, T = 4, 2, 256, 128, 9
+    G = 128
+    x = _rand_fp8((T, H), 1.0)
+    w1 = np.stack([_rand_fp8((2 * I, H), 0.05) for _ in range(E)])
+    w2 = np.stack([_rand_fp8((H, I), 0.05) for _ in range(E)])
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int64)
+    idx[3, 1] = -1
+    wts = rng.random((T, K)).astype(np.float32)
+    ref = orc.layer(x, None, w1, None, w2, None, idx, wts, E=E, G=G, scaled=False)
+    t = orc.e4m3_decode_table().astype(np.float64)
+    y = np.zeros((T, H))
+    for tok in range(T):
+        for k in range(K):
+            e = idx[tok, k]
+            if e < 0:
+                continue
+            wl = t[w1[e]]
+            h_idx = np.arange(I)
+            g = t[x[tok]] @ wl[(h_idx // G) * 2 * G + h_idx % G].T
+            u = t[x[tok]] @ wl[(h_idx // G) * 2 * G + h_idx % G + G].T
+            h = np.clip(g / (1 + np.exp(-g)) * u, -448, 448)
+            hq = torch.from_numpy(h.astype(np.float32)).to(torch.float8_e4m3fn).float().numpy()
+            o = hq.astype(np.float64) @ t[w2[e]].T
+            ob = torch.from_numpy(o.astype(np.float32)).to(torch.bfloat16).float().numpy()
+            y[tok] += ob * wts[tok, k]
+    rms = np.sqrt(np.mean(y ** 2))
+    assert np.abs(ref["y"] - y).max() <= 2e-2 * rms
