@@ -1,17 +1,26 @@
 // gemm.hip -- the two grouped fp8 GEMMs of the MoE layer on CDNA4 MFMA.
 //
+// Both GEMMs read fp8 e4m3 operands from HBM and convert them in registers,
+// exactly (UE8M0 scales folded in), to bf16 for v_mfma_f32_16x16x32_bf16.
+// gfx950's fp8 MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4 and
+// v_mfma_f32_16x16x32_fp8_fp8 alike) return exact products but sum them with
+// truncating alignment -- measured error up to ~2^-20 of sum|terms| against
+// ~1e-8 for the bf16 MFMA and for sequential fp32 -- which flips the L1 fp8
+// requantisation (and its 128-block scales) and the L2 bf16 rounding often
+// enough, against the reference's fp32 host path, to break the layer's
+// end-to-end tolerance.  The bf16 path keeps every sum fp32-accurate.
+//
 // L1 (reference: l1_gemm_swiglu_body_paired src/compute.cuh:280-484,
 //     r19_l1_big / r24_l1_big src/compute_big.cuh:320-515, 888-1161):
 //   for every work item (expert e, rows m0 .. m0+16*MT of e's slots) and every
-//   block of 128 hidden columns, g/u = W1_e[gate/up rows] . x[token]^T with
-//   v_mfma_scale_f32_16x16x128_f8f6f4 (fp32 accumulation, UE8M0 block scales
-//   applied by the instruction), then h = silu(g)*u and the fp8 cast of h
+//   block of 128 hidden columns, g/u = W1_e[gate/up rows] . x[token]^T, then
+//   h = silu(g)*u and the fp8 cast of h
 //   (raw RNE-saturating, or per-128 UE8M0 requant) into ffn[slot][I].
 //   The activation rows are gathered straight from x through perm[] (the
 //   fused DISPATCH gather: 16-byte loads of the routed tokens' rows).
 // L2 (reference: l2_gemm_body src/compute.cuh:497-641, r24_l2_big
 //     src/compute_big.cuh:1375-1679):
-//   o = W2_e . ffn[slot]^T, fp32 accumulation, bf16 RNE into l2[slot][H].
+//   o = W2_e . ffn[slot]^T, bf16 RNE into l2[slot][H].
 //
 // Operand roles: the weight tile is the MFMA "A" operand (16 output channels
 // x 128 k) and the 16 token rows are "B" (128 k x 16 tokens), so each lane's
@@ -56,24 +65,36 @@ __device__ __forceinline__ void load_stage(Stage<MT>& s, const uint8_t* const* w
     for (int j = 0; j < MT; ++j) s.sb[j] = xsf[j] ? (int)xsf[j][kt] : 127;
 }
 
-// acc[t][j] += tile t x token tile j; tiles 0,1 use scale sa[0], 2,3 sa[1].
-template <int MT>
-__device__ __forceinline__ void mma_stage(v4f (&acc)[4][MT], const Stage<MT>& s, int ntiles) {
+// bf16 MFMA step with fp32-accurate sums: each lane's 32 fp8 bytes per tile
+// are converted (scale folded in, exact) to four groups of 8 bf16, group q
+// feeding the q-th of four 16x16x32 MFMAs; A and B use the same grouping, so
+// every k of the 128-step meets its partner exactly once.
+struct MmaBf16 {
+    template <int MT>
+    __device__ __forceinline__ static void run(v4f (&acc)[4][MT], const Stage<MT>& s,
+                                               int ntiles) {
+        const float sa0 = ue8m0_to_f32(s.sa[0]), sa1 = ue8m0_to_f32(s.sa[1]);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const v8i a = join8(s.a[t][0], s.a[t][1]);
+        for (int q = 0; q < 4; ++q) {
+            const int h = q >> 1, d = 2 * (q & 1);
+            v8bf b[MT];
 #pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            if (j < ntiles) {
-                const v8i b = join8(s.b[j][0], s.b[j][1]);
-                acc[t][j] = mfma_fp8(a, b, acc[t][j], s.sa[t >> 1], s.sb[j]);
+            for (int j = 0; j < MT; ++j)
+                if (j < ntiles)
+                    b[j] = fp8x8_to_bf16(s.b[j][h][d], s.b[j][h][d + 1], ue8m0_to_f32(s.sb[j]));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const v8bf a = fp8x8_to_bf16(s.a[t][h][d], s.a[t][h][d + 1], t < 2 ? sa0 : sa1);
+#pragma unroll
+                for (int j = 0; j < MT; ++j)
+                    if (j < ntiles) acc[t][j] = mfma_bf16(a, b[j], acc[t][j]);
             }
         }
     }
-}
+};
 
 // K loop with an S-stage register pipeline over KT k-steps of 128.
-template <int MT, int S>
+template <class Mma, int MT, int S>
 __device__ __forceinline__ void gemm_mainloop(v4f (&acc)[4][MT], const uint8_t* const* wt,
                                               const uint8_t* const* xr, int KT,
                                               const uint8_t* wsf0, const uint8_t* wsf1,
@@ -88,7 +109,7 @@ __device__ __forceinline__ void gemm_mainloop(v4f (&acc)[4][MT], const uint8_t* 
             const int kt = kb + s;
             const int kl = kt + S - 1;
             if (kl < KT) load_stage<MT>(buf[(s + S - 1) % S], wt, xr, kl, wsf0, wsf1, xsf);
-            if (kt < KT) mma_stage<MT>(acc, buf[s], ntiles);
+            if (kt < KT) Mma::template run<MT>(acc, buf[s], ntiles);
         }
     }
 }
@@ -145,7 +166,7 @@ __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < MT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    gemm_mainloop<MT, stages_for<MT>()>(acc, wt, xr, KT, wsf0, wsf1, xsf, ntiles);
+    gemm_mainloop<MmaBf16, MT, stages_for<MT>()>(acc, wt, xr, KT, wsf0, wsf1, xsf, ntiles);
 
     // Epilogue: h = silu(g) * u for channels h0 + 16*pp + 4*(L/16) + i.
     float hv[MT][2][4];
@@ -249,7 +270,7 @@ __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < MT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    gemm_mainloop<MT, stages_for<MT>()>(acc, wt, xr, KT, wsf, wsf, xsf, ntiles);
+    gemm_mainloop<MmaBf16, MT, stages_for<MT>()>(acc, wt, xr, KT, wsf, wsf, xsf, ntiles);
 
 #pragma unroll
     for (int j = 0; j < MT; ++j) {

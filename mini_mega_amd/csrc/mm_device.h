@@ -1,6 +1,6 @@
 // mm_device.h -- device helpers shared by the gfx950 kernels of the fused
 // FP8xFP8 MoE layer: tile layout addressing, fp8 / bf16 / UE8M0 conversions
-// and the block-scaled MFMA wrapper.
+// and the MFMA wrapper.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,8 +17,9 @@ namespace mm {
 // k < 128) sits at
 //     ((k % 32) / 16) * 1024 + (r + 16 * (k / 32)) * 16 + (k % 16)
 // so that a wave loading 16 bytes per lane at lane*16 (+1024) reads 1 KiB
-// contiguous, and lane L ends up holding row L%16, k in [32*(L/16), +32): the
-// operand of one v_mfma_scale_f32_16x16x128_f8f6f4 for that lane.
+// contiguous, and lane L ends up holding row L%16, k in [32*(L/16), +32):
+// after an exact fp8 -> bf16 conversion, bytes 8q .. 8q+7 of that range are
+// the lane's operand of the q-th of four 16x16x32 bf16 MFMAs per 128 k.
 // Activations (x rows, ffn rows) are plain row-major and are loaded with the
 // same lane -> (row, k-range) assignment, so both MFMA operands agree on k.
 // ---------------------------------------------------------------------------
@@ -32,24 +33,36 @@ __host__ __device__ inline size_t tile_byte(int r, int k, int k_cols) {
            (size_t)(((kk & 31) >> 4) * 1024 + (rr + 16 * (kk >> 5)) * 16 + (kk & 15));
 }
 
-typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
-// One 16x16x128 fp8(e4m3) x fp8(e4m3) MFMA with E8M0 block scales
-// (127 = 2^0).  a: 16 rows (M) x 128 k, b: 128 k x 16 columns (N);
-// d lane L: column L%16, rows 4*(L/16) .. +3.
-__device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c,
-                                        int sa, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+// One 16x16x32 bf16 MFMA (fp32 accumulation): a 16 rows (M) x 32 k, b 32 k x
+// 16 columns (N).  Lane L supplies row / column L%16 and 8 consecutive k of
+// its k-group L/16, the same for both operands; d lane L holds column L%16,
+// rows 4*(L/16) .. +3.  Its sums are fp32-accurate (measured ~1e-8 of
+// sum|terms|), unlike gfx950's fp8 MFMAs (truncating, up to ~2^-20).
+__device__ __forceinline__ v4f mfma_bf16(const v8bf& a, const v8bf& b, const v4f& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ v8i join8(const v4i& lo, const v4i& hi) {
-    v8i r;
-    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-    return r;
+// Eight fp8 e4m3 bytes (two dwords, low byte first) -> eight bf16 values
+// multiplied by the power-of-two scale s: exact, since an e4m3 value has at
+// most 4 significant bits and bf16 keeps fp32's exponent range.
+__device__ __forceinline__ v8bf fp8x8_to_bf16(int d0, int d1, float s) {
+    const v2bf a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, s, false);
+    const v2bf b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, s, true);
+    const v2bf c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, s, false);
+    const v2bf d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, s, true);
+    const v4bf ab = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+    const v4bf cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+    return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
 }
+
+// UE8M0 exponent byte -> the float 2^(e-127) (e in [1, 254]).
+__device__ __forceinline__ float ue8m0_to_f32(int e) { return __uint_as_float((uint32_t)e << 23); }
 
 // fp32 -> OCP e4m3 byte pairs, round to nearest even, saturating at +-448:
 // the explicit clamp gives the saturation (the hardware conversion itself is

@@ -28,6 +28,13 @@
 
 #define ORC_API __attribute__((visibility("default")))
 
+/* Accumulation model of orc_l1_rows / orc_l2_rows: 0 = sequential fp32 (the
+ * reference host path), 1 = float64 accumulation rounded once to fp32 (an
+ * "exactly summing device" model used only to bound what any device can
+ * reach against the fp32 host path). */
+static int g_acc64 = 0;
+ORC_API void orc_set_acc64(int on) { g_acc64 = on; }
+
 /* ------------------------------------------------------------ E4M3 decode --
  * src/bench_check.cuh:327-358: exp=0 -> +-(m/8)*2^-6; exp 1..15 ->
  * +-(1+m/8)*2^(exp-7); 0x7F/0xFF -> NaN; max finite 448 = 0x7E. */
@@ -306,9 +313,19 @@ ORC_API void orc_l1_rows(const uint8_t* x, const uint8_t* xsf, int rows, const u
         for (int r = 0; r < rows; ++r) {
             const float* xr = xd + (size_t)r * H;
             float g = 0.0f, u = 0.0f;
-            for (int k = 0; k < H; ++k) {
-                g += xr[k] * wg[k];
-                u += xr[k] * wu[k];
+            if (g_acc64) {
+                double g64 = 0.0, u64 = 0.0;
+                for (int k = 0; k < H; ++k) {
+                    g64 += (double)xr[k] * wg[k];
+                    u64 += (double)xr[k] * wu[k];
+                }
+                g = (float)g64;
+                u = (float)u64;
+            } else {
+                for (int k = 0; k < H; ++k) {
+                    g += xr[k] * wg[k];
+                    u += xr[k] * wu[k];
+                }
             }
             out[(size_t)r * I + h] = (g / (1.0f + expf(-g))) * u;
         }
@@ -357,7 +374,13 @@ ORC_API void orc_l2_rows(const uint8_t* ffn, const uint8_t* fsf, int rows, const
         for (int r = 0; r < rows; ++r) {
             const float* ar = ad + (size_t)r * I;
             float acc = 0.0f;
-            for (int k = 0; k < I; ++k) acc += ar[k] * wr[k];
+            if (g_acc64) {
+                double a64 = 0.0;
+                for (int k = 0; k < I; ++k) a64 += (double)ar[k] * wr[k];
+                acc = (float)a64;
+            } else {
+                for (int k = 0; k < I; ++k) acc += ar[k] * wr[k];
+            }
             out[(size_t)r * H + n] = acc;
         }
     }

@@ -61,6 +61,7 @@ def lib():
         L.orc_quant_ffn.argtypes = [vp, i32, i32, i32, vp, vp]
         L.orc_l2_rows.argtypes = [vp, vp, i32, vp, vp, i32, i32, vp]
         L.orc_reduce.argtypes = [vp, vp, vp, i32, i32, i32, vp, vp]
+        L.orc_set_acc64.argtypes = [i32]
         L.orc_layer_slots.restype = i32
         L.orc_layer_slots.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32,
                                       i32, i32, vp, vp, vp, vp, i32]
@@ -203,8 +204,9 @@ def reduce(l2_bits: np.ndarray, pair_pos: np.ndarray, w: np.ndarray, T: int, top
 
 
 def layer(x, xsf, w1, w1sf, w2, w2sf, topk_idx, topk_w, E: int, G: int, scaled: bool,
-          nthreads: int = 8, expert_mask=None, cap: int | None = None):
+          nthreads: int = 8, expert_mask=None, cap: int | None = None, acc64: bool = False):
     """Full reference chain: route -> L1 -> quant -> L2 -> bf16 -> reduce.
+    acc64=True sums the GEMMs in float64 (an exactly-summing device model).
 
     Returns dict with counts/offsets/perm/pair_pos/ffn/ffn_sf/l2/y/y_bf16."""
     T, K = topk_idx.shape
@@ -217,10 +219,12 @@ def layer(x, xsf, w1, w1sf, w2, w2sf, topk_idx, topk_w, E: int, G: int, scaled: 
     l2 = np.zeros((max(slots, 1), H), np.uint16)
     perm_c = np.ascontiguousarray(np.concatenate([perm, np.zeros(1, np.uint32)]))
     mask = None if expert_mask is None else np.ascontiguousarray(expert_mask, np.uint8)
+    lib().orc_set_acc64(int(acc64))
     lib().orc_layer_slots(_p(np.ascontiguousarray(x)), _p(xsf), _p(np.ascontiguousarray(w1)),
                           _p(w1sf), _p(np.ascontiguousarray(w2)), _p(w2sf), _p(offsets),
                           _p(perm_c), K, E, H, I, G, int(scaled), _p(mask), _p(ffn),
                           _p(ffn_sf), _p(l2), nthreads)
+    lib().orc_set_acc64(0)
     y, yb = reduce(l2, pair_pos, topk_w, T, K)
     return dict(counts=counts, offsets=offsets, perm=perm, pair_pos=pair_pos,
                 ffn=ffn[:slots], ffn_sf=ffn_sf[:slots] if scaled else None, l2=l2[:slots],
