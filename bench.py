@@ -56,6 +56,21 @@ def layer_flops(T: int) -> float:
     return 6.0 * H * I * T * K
 
 
+def profiled_traffic(T: int, kernel_prefix: str):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC
+    summary (FETCH_SIZE / WRITE_SIZE scaled by the copy-kernel calibration),
+    or None when no summary exists for this workload."""
+    path = os.path.join(ROOT, "profiles", f"moe_layer_t{T}_traffic.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        d = json.load(f)
+    for name, v in d.get("kernels", {}).items():
+        if name.startswith(kernel_prefix):
+            return int(v["traffic_bytes"]), os.path.relpath(path, ROOT)
+    return None, None
+
+
 def time_events(fn, iters: int, stream) -> float:
     """Average ms per call of fn() measured with HIP events on `stream`."""
     import torch
@@ -116,6 +131,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-experts", type=int, default=32)
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain device copy of 2 GiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the whole layer on ONE GPU (all 256 experts); "
@@ -127,6 +144,19 @@ def main():
     from mini_mega_amd import inputs
 
     torch.cuda.set_device(0)
+    if args.copy_probe:
+        n = 2 << 30
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / 3
+        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n,
+                          "copy_GBs": round(2 * n / dt / 1e9, 1)}), flush=True)
+        return
     T = args.tokens
     print(f"[bench] setup T={T} zipf={args.zipf}", file=sys.stderr, flush=True)
     _, xq, xsf = inputs.make_x(T, H, seed=args.seed, scaled=True)
@@ -190,6 +220,7 @@ def main():
     b2 = l2_bytes(counts)
     a2 = b2 / (ms_l2 * 1e-3) / 1e9
 
+    traffic, traffic_src = profiled_traffic(T, "mm::l1_kernel")
     out = {
         "metric": "MoE layer µs + TFLOPS + HBM GB/s (% roofline), E256 top8 H6144 I2048, "
                   "T=512/2048/8192",
@@ -219,8 +250,8 @@ def main():
                       "bytes": b2},
         "roofline": {"bound": "hbm", "kernel": "l1_kernel (grouped gate/up GEMM + SwiGLU)",
                      "achieved": round(a1, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(a1 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes": b1},
+                     "frac": round(a1 / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src, "algorithmic_bytes": b1},
         "active_experts": int((counts > 0).sum()),
         "max_expert_rows": int(counts.max()),
     }
