@@ -27,10 +27,6 @@ int auto_m_tile(int tokens, int topk, int E) {
     return 64;
 }
 
-int m_tile_of(const MegaLaunchArgs& a) {
-    return a.win_cap > 0 ? a.win_cap : auto_m_tile(a.max_tokens, a.topk, a.num_experts);
-}
-
 int pairing_block(int I) { return I < 256 ? I : 256; }
 
 int check_dims(int topk, int E, int H, int I, int win_cap) {

@@ -84,8 +84,7 @@ class SymmBuffer:
     def __init__(self, group, num_experts: int, num_max_tokens_per_rank: int, num_topk: int,
                  hidden: int, intermediate_hidden: int, num_shared_experts: int = 0,
                  mma_type: str = "fp8xfp8", activation: str = "swiglu",
-                 grid_num_tokens: Optional[int] = None, expert_window: Optional[int] = None,
-                 use_ue8m0: bool = False):
+                 grid_num_tokens: Optional[int] = None, expert_window: Optional[int] = None):
         if activation != "swiglu":
             raise ValueError(f"Only `swiglu` activation is supported, got `{activation}`")
         if mma_type not in _SUPPORTED_MMA_TYPES:
@@ -112,7 +111,6 @@ class SymmBuffer:
         self.mma_type = mma_type
         self.activation = activation
         self.expert_window = ew
-        self.use_ue8m0 = bool(use_ue8m0)
         self.device = torch.cuda.current_device()
         cap = self.num_max_tokens_per_rank
         self.layout = _lib.layout(cap, self.num_topk, self.num_experts, self.hidden,
@@ -206,14 +204,13 @@ def get_symm_buffer_for_mega_moe(group, num_experts: int, num_max_tokens_per_ran
                                  use_fp8_dispatch: Optional[bool] = None,
                                  mma_type: str = "fp8xfp8", activation: str = "swiglu",
                                  num_tokens: Optional[int] = None,
-                                 expert_window: Optional[int] = None,
-                                 use_ue8m0: bool = False) -> SymmBuffer:
+                                 expert_window: Optional[int] = None) -> SymmBuffer:
     if use_fp8_dispatch is not None:
         assert use_fp8_dispatch == (mma_type.split("x")[0] == "fp8")
     return SymmBuffer(group, num_experts, num_max_tokens_per_rank, num_topk, hidden,
                       intermediate_hidden, num_shared_experts, mma_type=mma_type,
                       activation=activation, grid_num_tokens=num_tokens,
-                      expert_window=expert_window, use_ue8m0=use_ue8m0)
+                      expert_window=expert_window)
 
 
 def _split(w):
