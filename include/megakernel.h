@@ -59,7 +59,7 @@ struct MegaLaunchArgs {
     int R = 1, rank = 0;         // single GPU: R = 1, rank = 0
     int tokens = 0;              // tokens in this launch
     int slot_capacity = 0;       // per-expert slot cap; 0 = no cap (tokens*topk)
-    int win_cap = 0;             // rows per work item (M tile); 0 = auto
+    int win_cap = 0;             // max rows per work item: 0 (auto), 16, 32, 64, 128
     int grid = 0, threads = 0;   // informational (filled by make_args)
     int64_t smem = 0;
 
@@ -109,7 +109,7 @@ struct MegaLayout {
     int64_t chunk_hist;    // int32[nchunks][E] per-chunk histograms -> prefixes
     int64_t counts;        // int32[E]   per-expert routed rows (after cap)
     int64_t offsets;       // int32[E+1] exclusive prefix of counts
-    int64_t items;         // int32[max_items][2] (expert, first row) work items
+    int64_t items;         // int32[max_items][4] (expert, first row, end row, 0) work items
     int64_t perm;          // uint32[P]  pair index per slot (canonical order)
     int64_t pair_pos;      // int32[P]   slot per pair or -1
     int64_t xq;            // uint8[max_tokens][H]     folded fp8 x (in_bf16)

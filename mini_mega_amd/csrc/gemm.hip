@@ -121,9 +121,10 @@ template <int MT>
 __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
     const int item = blockIdx.y;
     if (item >= p.status[1]) return;
-    const int e = p.items[2 * item], m0 = p.items[2 * item + 1];
-    const int cnt = p.counts[e], off = p.offsets[e];
-    const int rows = min(cnt - m0, MT * 16);
+    const int4 it = reinterpret_cast<const int4*>(p.items)[item];
+    const int e = it.x, m0 = it.y;
+    const int cnt = it.z, off = p.offsets[e];  // rows m0 .. cnt-1 of expert e
+    const int rows = cnt - m0;
     const int ntiles = (rows + 15) >> 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, G = p.G, KT = H >> 7;
@@ -238,9 +239,10 @@ template <int MT>
 __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
     const int item = blockIdx.y;
     if (item >= p.status[1]) return;
-    const int e = p.items[2 * item], m0 = p.items[2 * item + 1];
-    const int cnt = p.counts[e], off = p.offsets[e];
-    const int rows = min(cnt - m0, MT * 16);
+    const int4 it = reinterpret_cast<const int4*>(p.items)[item];
+    const int e = it.x, m0 = it.y;
+    const int cnt = it.z, off = p.offsets[e];  // rows m0 .. cnt-1 of expert e
+    const int rows = cnt - m0;
     const int ntiles = (rows + 15) >> 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, KT = I >> 7;
@@ -290,9 +292,7 @@ __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
 
 template __global__ void l1_kernel<1>(GemmParams);
 template __global__ void l1_kernel<2>(GemmParams);
-template __global__ void l1_kernel<4>(GemmParams);
 template __global__ void l2_kernel<1>(GemmParams);
 template __global__ void l2_kernel<2>(GemmParams);
-template __global__ void l2_kernel<4>(GemmParams);
 
 }  // namespace mm

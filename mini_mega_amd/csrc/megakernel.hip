@@ -21,10 +21,13 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
 int auto_m_tile(int tokens, int topk, int E) {
     // Rows per work item: one item per expert when the expected expert load
-    // fits, so that each expert's weights stream from HBM once.
+    // (plus the spread of a random router) fits, so that each expert's weights
+    // stream from HBM once.  <= 32 rows: decode-shaped kernels; 64..256: the
+    // 8-wave LDS-staged kernels.
     const double mean = (double)tokens * topk / (E > 0 ? E : 1);
     if (mean <= 20.0) return 32;
-    return 64;
+    if (mean <= 44.0) return 64;
+    return 128;
 }
 
 int pairing_block(int I) { return I < 256 ? I : 256; }
@@ -32,8 +35,10 @@ int pairing_block(int I) { return I < 256 ? I : 256; }
 int check_dims(int topk, int E, int H, int I, int win_cap) {
     if (topk < 1 || topk > 64 || E < 1 || E > mm::kMaxExperts) return kErrBadDims;
     if (H < 256 || H % 256 != 0 || I < 128 || I % 128 != 0) return kErrBadDims;
+    if (H > 128 * mm::kBigMaxKT || I > 128 * mm::kBigMaxKT) return kErrBadDims;
     if (I % pairing_block(I) != 0) return kErrBadDims;
-    if (win_cap != 0 && win_cap != 16 && win_cap != 32 && win_cap != 64) return kErrBadDims;
+    if (win_cap != 0 && win_cap != 16 && win_cap != 32 && win_cap != 64 && win_cap != 128)
+        return kErrBadDims;
     return kOk;
 }
 
@@ -128,12 +133,26 @@ mm::GemmParams gemm_params(const MegaLaunchArgs& a, const Bound& b) {
     return p;
 }
 
-void launch_gemm(void (*k1)(mm::GemmParams), void (*k2)(mm::GemmParams),
-                 void (*k4)(mm::GemmParams), int m_tile, dim3 grid, hipStream_t s,
+using GemmKernel = void (*)(mm::GemmParams);
+
+// Decode-shaped (4 waves, MT = 1, 2) for m_tile <= 32; LDS-staged 8-wave
+// kernels (MT = 4, 8) above.
+void launch_gemm(const GemmKernel (&small)[2], const GemmKernel (&big)[2], int m_tile,
+                 int nblocks_small, int nblocks_big, int max_items, hipStream_t s,
                  const mm::GemmParams& p) {
-    void (*k)(mm::GemmParams) = m_tile <= 16 ? k1 : (m_tile <= 32 ? k2 : k4);
-    hipLaunchKernelGGL(k, grid, dim3(mm::kGemmThreads), 0, s, p);
+    if (m_tile <= 32) {
+        hipLaunchKernelGGL(small[m_tile <= 16 ? 0 : 1], dim3(nblocks_small, max_items),
+                           dim3(mm::kGemmThreads), 0, s, p);
+    } else {
+        const int i = m_tile <= 64 ? 0 : 1;
+        hipLaunchKernelGGL(big[i], dim3(nblocks_big, max_items), dim3(mm::kBigThreads), 0, s, p);
+    }
 }
+
+const GemmKernel kL1Small[2] = {mm::l1_kernel<1>, mm::l1_kernel<2>};
+const GemmKernel kL1Big[2] = {mm::l1_big_kernel<4>, mm::l1_big_kernel<8>};
+const GemmKernel kL2Small[2] = {mm::l2_kernel<1>, mm::l2_kernel<2>};
+const GemmKernel kL2Big[2] = {mm::l2_big_kernel<4>, mm::l2_big_kernel<8>};
 
 int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     Bound b;
@@ -147,8 +166,8 @@ int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     p.w_sf = a.w1_sf;
     p.out8 = b.ws + b.L.ffn;
     p.out_sf = b.ws + b.L.ffn_sf;
-    const dim3 grid(a.intermediate / mm::kL1BlockH, b.L.max_items);
-    launch_gemm(mm::l1_kernel<1>, mm::l1_kernel<2>, mm::l1_kernel<4>, b.m_tile, grid, s, p);
+    const int nb = a.intermediate / mm::kL1BlockH;
+    launch_gemm(kL1Small, kL1Big, b.m_tile, nb, nb, b.L.max_items, s, p);
     return launched(kOk);
 }
 
@@ -163,8 +182,8 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     p.w = a.w2;
     p.w_sf = a.w2_sf;
     p.out16 = at<uint16_t>(b, b.L.l2);
-    const dim3 grid(a.hidden / mm::kL2BlockN, b.L.max_items);
-    launch_gemm(mm::l2_kernel<1>, mm::l2_kernel<2>, mm::l2_kernel<4>, b.m_tile, grid, s, p);
+    const int nb = a.hidden / mm::kL2BlockN;
+    launch_gemm(kL2Small, kL2Big, b.m_tile, nb, nb, b.L.max_items, s, p);
     return launched(kOk);
 }
 
@@ -235,7 +254,7 @@ MegaLayout layout(int max_tokens, int topk, int num_experts, int hidden, int int
     L.chunk_hist = o;  o = align256(o + (int64_t)L.nchunks * E * 4);
     L.counts = o;      o = align256(o + E * 4);
     L.offsets = o;     o = align256(o + (E + 1) * 4);
-    L.items = o;       o = align256(o + (int64_t)L.max_items * 8);
+    L.items = o;       o = align256(o + (int64_t)L.max_items * 16);
     L.perm = o;        o = align256(o + P * 4);
     L.pair_pos = o;    o = align256(o + P * 4);
     L.xq = o;          o = align256(o + (int64_t)max_tokens * hidden);
@@ -324,10 +343,12 @@ void dump_kernel_resources() {
     print_attr("route_scatter", (const void*)mm::route_scatter_kernel);
     print_attr("l1_kernel<1>", (const void*)mm::l1_kernel<1>);
     print_attr("l1_kernel<2>", (const void*)mm::l1_kernel<2>);
-    print_attr("l1_kernel<4>", (const void*)mm::l1_kernel<4>);
+    print_attr("l1_big_kernel<4>", (const void*)mm::l1_big_kernel<4>);
+    print_attr("l1_big_kernel<8>", (const void*)mm::l1_big_kernel<8>);
     print_attr("l2_kernel<1>", (const void*)mm::l2_kernel<1>);
     print_attr("l2_kernel<2>", (const void*)mm::l2_kernel<2>);
-    print_attr("l2_kernel<4>", (const void*)mm::l2_kernel<4>);
+    print_attr("l2_big_kernel<4>", (const void*)mm::l2_big_kernel<4>);
+    print_attr("l2_big_kernel<8>", (const void*)mm::l2_big_kernel<8>);
     print_attr("combine", (const void*)mm::combine_kernel);
     std::fflush(stdout);
 }

@@ -12,7 +12,9 @@ constexpr int kScanThreads = 1024;
 constexpr int kRouteThreads = 256;
 constexpr int kRouteChunk = 1024;   // pairs per routing chunk
 
-constexpr int kGemmThreads = 256;   // 4 waves per workgroup
+constexpr int kGemmThreads = 256;   // 4 waves per workgroup (decode-shaped GEMMs)
+constexpr int kBigThreads = 512;    // 8 waves per workgroup (large-M GEMMs)
+constexpr int kBigMaxKT = 64;       // large-M GEMMs: K / 128 <= 64 (H, I <= 8192)
 constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 workgroup
 constexpr int kL2BlockN = 256;      // output channels per L2 workgroup
 
@@ -25,7 +27,7 @@ struct GemmParams {
     const uint8_t* w_sf;      // UE8M0 block scales [E][N/128][K/128] or null
     const int* counts;        // [E]
     const int* offsets;       // [E+1]
-    const int* items;         // [max_items][2]
+    const int* items;         // [max_items][4]: expert, first row, end row, 0
     const int* status;        // [1] = number of items
     const uint32_t* perm;     // slot -> pair (L1 gathers x rows through it)
     uint8_t* out8;            // L1: ffn fp8 [P][I]
@@ -35,8 +37,15 @@ struct GemmParams {
     int ffn_ue8m0;
 };
 
+// Scale byte 127 (2^0) read with stride 0 when an operand carries no scales,
+// so scale loads are unconditional (no branch in the k loops).
+__device__ const uint8_t kUnitScale[16] = {127, 127, 127, 127, 127, 127, 127, 127,
+                                          127, 127, 127, 127, 127, 127, 127, 127};
+
 template <int MT> __global__ void l1_kernel(GemmParams p);
 template <int MT> __global__ void l2_kernel(GemmParams p);
+template <int MT> __global__ void l1_big_kernel(GemmParams p);
+template <int MT> __global__ void l2_big_kernel(GemmParams p);
 
 __global__ void route_hist_kernel(const int64_t*, int, int, int*);
 __global__ void route_scan_kernel(int*, int, int, int, int, int, int*, int*, int*, int*);

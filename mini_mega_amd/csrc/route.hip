@@ -85,14 +85,18 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
     const int off = block_exclusive_scan(cnt, smem, &slots);
     if (e < E) offsets[e] = off;
     if (threadIdx.x == 0) offsets[E] = slots;
+    // Work items: the expert's rows split evenly into ceil(cnt / m_tile)
+    // items of at most m_tile rows (no item re-streams the expert's weights
+    // for a small remainder).
     const int nm = (cnt + m_tile - 1) / m_tile;
+    const int sz = nm > 0 ? (cnt + nm - 1) / nm : 0;
     int nitems = 0;
     const int ioff = block_exclusive_scan(nm, smem, &nitems);
     for (int j = 0; j < nm; ++j) {
         const int it = ioff + j;
         if (it < max_items) {
-            items[2 * it + 0] = e;
-            items[2 * it + 1] = j * m_tile;
+            const int m0 = j * sz;
+            reinterpret_cast<int4*>(items)[it] = make_int4(e, m0, min(cnt, m0 + sz), 0);
         }
     }
     if (threadIdx.x == 0) {

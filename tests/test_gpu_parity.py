@@ -188,6 +188,11 @@ SMALL = [
     (32, 8, 1024, 512, 200, False, 16),
     (16, 4, 512, 256, 300, True, 64),
     (64, 8, 512, 256, 96, True, 32),
+    # LDS-staged 8-wave kernels (work items of 64..256 rows, rows split evenly)
+    (32, 8, 1024, 512, 160, False, 64),
+    (16, 4, 512, 256, 600, True, 128),
+    (8, 8, 256, 128, 300, True, 128),    # every token routed to every expert: 3 items each
+    (24, 6, 1024, 512, 700, True, 0),    # auto tile: 175 rows per expert -> 2 items of <= 128
 ]
 
 
@@ -245,7 +250,7 @@ def test_checkcu_inputs_full_size_t512():
 
 
 # ------------------------------------------------------------ full sizes --
-@pytest.mark.parametrize("T,zipf", [(512, None), (2048, None), (2048, 1.1)])
+@pytest.mark.parametrize("T,zipf", [(512, None), (2048, None), (2048, 1.1), (8192, None)])
 def test_full_size_layer(T, zipf):
     """BASELINE configs 1, 2, 4 at full size: routing exact, staged L1/L2 on
     the busiest / a median / the lightest expert, REDUCE bit-exact, and the
