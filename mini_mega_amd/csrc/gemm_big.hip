@@ -1,54 +1,68 @@
 // gemm_big.hip -- the L1 / L2 grouped GEMMs for large per-expert row counts
-// (work items of 64..128 token rows: T >= ~1024 and skewed routing), where
+// (work items of 33..192 token rows: T >= ~1024 and skewed routing), where
 // the decode-shaped kernels of gemm.hip would re-stream each expert's weights
 // once per 32 rows.
 //
 // Reference counterparts: r24_l1_big / r24_l2_big (src/compute_big.cuh:888-1161,
 // 1375-1679), the reference's count-tiered big-window GEMMs.
 //
-// One 8-wave workgroup per (work item, block of 256 weight rows); each wave
-// owns a 32-row weight slice across all of the item's token rows (every weight
-// byte is loaded and converted exactly once):
-//   * per 128-k step, all 512 threads gather the item's BM = 16*MT activation
-//     rows (through perm[] for L1, slot order for L2), convert them once to
-//     bf16 with the row's UE8M0 scale folded in (exact), and store them in a
+// One 4-wave workgroup (one wave per SIMD) per work unit = (work item, block
+// of 256 weight rows); each wave owns a 64-row weight slice (four 16-row
+// tiles) across all of the item's token rows, so every weight byte is loaded
+// and converted exactly once and every activation operand read from LDS feeds
+// four MFMAs:
+//   * per 128-k step, the 256 threads gather the item's active token rows
+//     (through perm[] for L1, slot order for L2), convert them once to bf16
+//     with the row's UE8M0 scale folded in (exact), and store them in a
 //     double-buffered LDS tile: [token tile][k-group q][lane][8 bf16], so that
 //     a wave's operand read for one MFMA is 1 KiB contiguous;
-//   * each wave streams its two 16-row weight tiles (L1: gate and up rows of
-//     16 hidden columns; L2: 32 output channels) from HBM through a 4-stage
-//     register pipeline and converts them exactly to bf16;
+//   * each wave streams its four weight tiles (L1: gate and up rows of 32
+//     hidden columns; L2: 64 output channels) from HBM through a 3- or
+//     4-stage register pipeline and converts them exactly to bf16;
 //   * v_mfma_f32_16x16x32_bf16 (fp32-accurate sums; see gemm.hip) over the
 //     item's NT active token tiles -- NT is a compile-time specialisation
-//     picked per item, so there is no per-tile branch in the k loop and the
-//     2*NT accumulators are independent chains;
+//     picked per item (1..8, then even up to 12), so the k loop has no branch
+//     and the 4*NT accumulators (up to 192 registers) are independent chains;
 //   * epilogues as in gemm.hip: L1 SwiGLU + fp8 (raw, or per-128 UE8M0 with
-//     the 128-column amax reduced over the 8 waves in LDS), L2 bf16.
+//     the 128-column amax reduced over the 4 waves in LDS), L2 bf16.
+// Work units are numbered so that each XCD runs a contiguous range of them:
+// the N-blocks of one item share that XCD's L2 for the item's activations.
 #include "mm_kernels.h"
 
 namespace mm {
 
 constexpr int kXTileBytes = 16 * kTileK * 2;   // one bf16 token tile: 16 rows x 128 k
+constexpr int kWT = 4;                          // weight tiles per wave
+constexpr int kBigRows = kBigMaxTiles * 16;     // token rows per work item (max)
 
-template <int MT>
-struct BigSmem {
-    uint8_t x[2][MT * kXTileBytes];            // bf16 tiles, double buffered
-    uint8_t sfx[MT * 16][kBigMaxKT];           // the item's row scales, all k-steps
-    uint8_t sfw[16][kBigMaxKT];                // the block's 16 weight tiles' scales
+struct alignas(16) BigSmem {
+    uint8_t x[2][kBigMaxTiles * kXTileBytes];   // bf16 tiles, double buffered
+    uint8_t sfx[kBigMaxKT][kBigRows];           // the item's row scales [k-step][row]
+    uint8_t sfw[kBigMaxKT][4 * kWT];            // the block's 16 weight tiles' scales
 };
 
-// Loader: chunk i = tid + 512*u is row r = 16*(i/128) + i%16 of the item,
-// fp8 bytes [16*cc, 16*cc+16) of the k-step with cc = (i/16)%8: k-group
-// g = cc/2, MFMA groups q = 2*(cc%2) and q+1.  Rows vary fastest, so the 16
-// lanes of an LDS write phase fill 16 consecutive 16-byte slots (no bank
-// conflicts).  Two register stages: the rows of k-step kt+2 are in flight
-// while kt+1 is written to LDS.  Row addresses are 32-bit offsets.
-template <int MT>
+// Loader for NT active token tiles: chunk i = tid + 256*u is row
+// r = 16*(i/128) + i%16 of the item, fp8 bytes [16*cc, 16*cc+16) of the
+// k-step with cc = (i/16)%8: k-group g = cc/2, MFMA groups q = 2*(cc%2) and
+// q+1.  Rows vary fastest, so the 16 lanes of an LDS write phase fill 16
+// consecutive 16-byte slots (no bank conflicts).  For odd NT the upper half
+// of the last round re-does the chunk 128 below it (same bytes to the same
+// LDS slot), which keeps every thread's work uniform.  XS register stages:
+// with two (NT <= 8), the rows of k-step kt+2 are in flight while kt+1 is
+// written to LDS; with one (larger NT: registers go to accumulators, and a
+// k-step's MFMAs alone cover an L2 hit), kt+1 is loaded during step kt.
+template <int NT>
 struct XLoader {
-    static constexpr int U = MT / 4;
+    static constexpr int U = (NT * 128 + kBigThreads - 1) / kBigThreads;
+    static constexpr int XS = NT > 8 ? 1 : 2;
     const uint8_t* base;
     uint32_t off[U];
-    v4i reg[2][U];
+    v4i reg[XS][U];
 
+    __device__ __forceinline__ static int chunk(int u) {
+        const int i = threadIdx.x + kBigThreads * u;
+        return i < NT * 128 ? i : i - 128;
+    }
     __device__ __forceinline__ static int row_of(int i) { return ((i >> 7) << 4) | (i & 15); }
     __device__ __forceinline__ static int cc_of(int i) { return (i >> 4) & 7; }
 
@@ -56,15 +70,15 @@ struct XLoader {
 #pragma unroll
         for (int u = 0; u < U; ++u) reg[rs][u] = load16(base + off[u] + kt * kTileK);
     }
-    __device__ __forceinline__ void commit(BigSmem<MT>& sm, int stage, int rs, int kt) {
+    __device__ __forceinline__ void commit(BigSmem& sm, int stage, int rs, int kt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int i = threadIdx.x + kBigThreads * u;
+            const int i = chunk(u);
             const int r = row_of(i), cc = cc_of(i);
             const int lane_slot = (r & 15) + 16 * (cc >> 1);
             const int q0 = 2 * (cc & 1);
             uint8_t* t = &sm.x[stage][(r >> 4) * kXTileBytes + q0 * 1024 + lane_slot * 16];
-            const float s = ue8m0_to_f32(sm.sfx[r][kt]);
+            const float s = ue8m0_to_f32(sm.sfx[kt][r]);
             *reinterpret_cast<v8bf*>(t) = fp8x8_to_bf16(reg[rs][u][0], reg[rs][u][1], s);
             *reinterpret_cast<v8bf*>(t + 1024) = fp8x8_to_bf16(reg[rs][u][2], reg[rs][u][3], s);
         }
@@ -72,174 +86,290 @@ struct XLoader {
 };
 
 struct WStage {
-    v4i a[2][2];   // two weight tiles, two 16-byte halves each
+    v4i a[kWT][2];   // four weight tiles, two 16-byte halves each
 };
 
 __device__ __forceinline__ void w_load(WStage& w, const uint8_t* const* wt, int kt) {
     const size_t o = (size_t)kt * kTileBytes;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < kWT; ++t) {
         w.a[t][0] = load16_stream(wt[t] + o);
         w.a[t][1] = load16_stream(wt[t] + o + 1024);
     }
 }
 
-// acc[t][j] += weight tile t x token tile j, j < NT, one 128-k step.
-template <int MT, int NT>
-__device__ __forceinline__ void big_mma(v4f (&acc)[2][NT], const WStage& w,
-                                        const BigSmem<MT>& sm, int stage, int kt) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float s0 = ue8m0_to_f32(sm.sfw[2 * wave][kt]);
-    const float s1 = ue8m0_to_f32(sm.sfw[2 * wave + 1][kt]);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const v8bf a0 = fp8x8_to_bf16(w.a[0][q >> 1][2 * (q & 1)], w.a[0][q >> 1][2 * (q & 1) + 1], s0);
-        const v8bf a1 = fp8x8_to_bf16(w.a[1][q >> 1][2 * (q & 1)], w.a[1][q >> 1][2 * (q & 1) + 1], s1);
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const v8bf b = *reinterpret_cast<const v8bf*>(
-                &sm.x[stage][j * kXTileBytes + q * 1024 + lane * 16]);
-            acc[0][j] = mfma_bf16(a0, b, acc[0][j]);
-            acc[1][j] = mfma_bf16(a1, b, acc[1][j]);
-        }
-    }
+// Weight tile t's operand of k-group q (8 bf16 per lane) with scale s folded in.
+__device__ __forceinline__ v8bf w_group(const WStage& w, int t, int q, float s) {
+    return fp8x8_to_bf16(w.a[t][q >> 1][2 * (q & 1)], w.a[t][q >> 1][2 * (q & 1) + 1], s);
 }
 
-constexpr int kBigStages = 4;   // weight register stages (even: x stages alternate)
+// The wave's four weight-tile scale bytes of k-step kt (byte t = tile t).
+__device__ __forceinline__ uint32_t w_scales(const BigSmem& sm, int kt) {
+    const int wave = threadIdx.x >> 6;
+    return *reinterpret_cast<const uint32_t*>(&sm.sfw[kt][kWT * wave]);
+}
 
-// One k-step of the pipeline: prefetch activations for kt+2 and weights for
-// kt+S-1 (indices clamped to the last step: a redundant in-bounds reload
-// keeps the loop free of branches, so the compiler's wait counts stay
-// partial), compute kt, write the activations of kt+1 to LDS, barrier.  All
-// scale bytes come from LDS, so the only vector-memory loads in the loop are
-// the prefetches themselves.
-template <int MT, int NT, int S, int s>
-__device__ __forceinline__ void big_step(v4f (&acc)[2][NT], BigSmem<MT>& sm, XLoader<MT>& xl,
-                                         WStage (&w)[S], const uint8_t* const* wt, int kt,
-                                         int KT) {
-    xl.issue(min(kt + 2, KT - 1), s & 1);
+__device__ __forceinline__ float scale_of(uint32_t bytes, int t) {
+    return ue8m0_to_f32((bytes >> (8 * t)) & 0xffu);
+}
+
+// Weight register stages: 4 for NT <= 8 (even, so that two activation
+// stages alternate within a group), 3 above (a k-step of >= 160 MFMAs per
+// wave covers the latency of two steps ahead).
+template <int NT>
+constexpr int big_stages() { return NT > 8 ? 3 : 4; }
+
+constexpr int kBigReadAhead = 2;   // activation operand reads in flight ahead of their MFMAs
+
+// One k-step, software-pipelined by hand.  The step's 4*NT chunks (k-group
+// q, token tile j) each hold: the LDS read of the activation operand two
+// chunks ahead, a share of the conversions of the next k-group's weight
+// operands (in the last group: the next k-step's first), a share of the
+// activation commit of k-step kt+1 (last group only), and the chunk's 4
+// MFMAs.  A scheduling fence closes every chunk, so the compiler keeps this
+// order: operand reads stay two chunks ahead of their use, and conversions
+// overlap the MFMAs instead of stalling them.  Before the chunks: the
+// prefetches of activations (kt+XS) and weights (kt+S-1), with indices
+// clamped to the last step (a redundant in-bounds reload keeps the loop free
+// of branches, so the compiler's wait counts stay partial).  After: the
+// barrier that publishes the committed activations.  a0 carries the
+// converted k-group-0 operand from one step to the next.
+template <int NT, int S, int s>
+__device__ __forceinline__ void big_step(v4f (&acc)[kWT][NT], BigSmem& sm, XLoader<NT>& xl,
+                                         WStage (&w)[S], const uint8_t* const* wt,
+                                         v8bf (&a0)[kWT], int kt, int KT) {
+    constexpr int XS = XLoader<NT>::XS, U = XLoader<NT>::U;
+    constexpr int G = 4 * NT, D = kBigReadAhead;
+    constexpr int rs = XS == 2 ? ((s + 1) & 1) : 0;   // register stage holding k-step kt+1
+    const int lane = threadIdx.x & 63;
+    xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
     w_load(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));
-    // keep the prefetch loads ahead of this step's MFMAs
+    // scale bytes, read here and decoded where used (no wait before the MFMAs)
+    const int kn = min(kt + 1, KT - 1);
+    const uint32_t sc = w_scales(sm, kt), sn = w_scales(sm, kn);
+    uint32_t xs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) xs[u] = sm.sfx[kn][XLoader<NT>::row_of(XLoader<NT>::chunk(u))];
+    const uint8_t* xb = &sm.x[kt & 1][lane * 16];
+    uint8_t* xw = &sm.x[(kt + 1) & 1][0];
+    v8bf b[D + 1];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        b[d] = *reinterpret_cast<const v8bf*>(xb + (d % NT) * kXTileBytes + (d / NT) * 1024);
     __builtin_amdgcn_sched_barrier(0);
-    big_mma<MT, NT>(acc, w[s], sm, kt & 1, kt);
-    __builtin_amdgcn_sched_barrier(0);
-    xl.commit(sm, (kt + 1) & 1, (s + 1) & 1, min(kt + 1, KT - 1));
+    v8bf ac[kWT], an[kWT];
+#pragma unroll
+    for (int t = 0; t < kWT; ++t) ac[t] = a0[t];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int q = g / NT, j = g % NT;
+        if (g + D < G) {
+            const int gn = g + D;
+            b[gn % (D + 1)] = *reinterpret_cast<const v8bf*>(xb + (gn % NT) * kXTileBytes +
+                                                             (gn / NT) * 1024);
+        }
+#pragma unroll
+        for (int t = 0; t < kWT; ++t)
+            if (j == (t * NT) / kWT)
+                an[t] = q < 3 ? w_group(w[s], t, q + 1, scale_of(sc, t))
+                              : w_group(w[(s + 1) % S], t, 0, scale_of(sn, t));
+        if (q == 3) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (j == (u * NT) / U) {
+                    const int i = XLoader<NT>::chunk(u);
+                    const int r = XLoader<NT>::row_of(i), cc = XLoader<NT>::cc_of(i);
+                    uint8_t* t = xw + (r >> 4) * kXTileBytes + 2 * (cc & 1) * 1024 +
+                                 ((r & 15) + 16 * (cc >> 1)) * 16;
+                    const float sx = ue8m0_to_f32(xs[u]);
+                    *reinterpret_cast<v8bf*>(t) =
+                        fp8x8_to_bf16(xl.reg[rs][u][0], xl.reg[rs][u][1], sx);
+                    *reinterpret_cast<v8bf*>(t + 1024) =
+                        fp8x8_to_bf16(xl.reg[rs][u][2], xl.reg[rs][u][3], sx);
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < kWT; ++t) acc[t][j] = mfma_bf16(ac[t], b[g % (D + 1)], acc[t][j]);
+        if (j == NT - 1) {
+#pragma unroll
+            for (int t = 0; t < kWT; ++t) ac[t] = an[t];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < kWT; ++t) a0[t] = ac[t];
     __syncthreads();
 }
 
-template <int MT, int NT, int S, int s>
-__device__ __forceinline__ void big_group(v4f (&acc)[2][NT], BigSmem<MT>& sm, XLoader<MT>& xl,
-                                          WStage (&w)[S], const uint8_t* const* wt, int kb,
-                                          int KT) {
-    big_step<MT, NT, S, s>(acc, sm, xl, w, wt, kb + s, KT);
-    if constexpr (s + 1 < S) big_group<MT, NT, S, s + 1>(acc, sm, xl, w, wt, kb, KT);
+template <int NT, int S, int s>
+__device__ __forceinline__ void big_group(v4f (&acc)[kWT][NT], BigSmem& sm, XLoader<NT>& xl,
+                                          WStage (&w)[S], const uint8_t* const* wt,
+                                          v8bf (&a0)[kWT], int kb, int KT) {
+    big_step<NT, S, s>(acc, sm, xl, w, wt, a0, kb + s, KT);
+    if constexpr (s + 1 < S) big_group<NT, S, s + 1>(acc, sm, xl, w, wt, a0, kb, KT);
 }
 
 // Main loop: every wave runs the same KT + 1 barriers.  Activations: LDS
-// double buffer fed from two register stages.  Weights: S register stages.
+// double buffer fed from XS register stages.  Weights: S register stages.
 // Whole groups of S k-steps run without any branch; a remainder (only when
-// KT is not a multiple of S: tiny shapes) runs through the guarded tail.
-template <int MT, int NT>
-__device__ __forceinline__ void big_mainloop(v4f (&acc)[2][NT], BigSmem<MT>& sm,
-                                             XLoader<MT>& xl, const uint8_t* const* wt, int KT) {
-    constexpr int S = kBigStages;
+// KT is not a multiple of S) runs through the guarded tail.
+template <int NT>
+__device__ __forceinline__ void big_mainloop(v4f (&acc)[kWT][NT], BigSmem& sm, XLoader<NT>& xl,
+                                             const uint8_t* const* wt, int KT) {
+    constexpr int S = big_stages<NT>();
+    constexpr int XS = XLoader<NT>::XS;
+    static_assert(XS == 1 || S % 2 == 0, "two activation stages alternate within a group");
     WStage w[S];
+#pragma unroll
+    for (int t = 0; t < kWT; ++t)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
     xl.issue(0, 0);
-    xl.issue(min(1, KT - 1), 1);
+    if constexpr (XS == 2) xl.issue(min(1, KT - 1), 1);
 #pragma unroll
     for (int s = 0; s < S - 1; ++s) w_load(w[s], wt, min(s, KT - 1));
     xl.commit(sm, 0, 0, 0);
     __syncthreads();
+    v8bf a0[kWT];
+    {
+        const uint32_t sc = w_scales(sm, 0);
+#pragma unroll
+        for (int t = 0; t < kWT; ++t) a0[t] = w_group(w[0], t, 0, scale_of(sc, t));
+    }
     const int KF = KT - KT % S;
 #pragma unroll 1
-    for (int kb = 0; kb < KF; kb += S) big_group<MT, NT, S, 0>(acc, sm, xl, w, wt, kb, KT);
-    if (KF < KT) {
-        big_step<MT, NT, S, 0>(acc, sm, xl, w, wt, KF, KT);
-        if (KF + 1 < KT) big_step<MT, NT, S, 1>(acc, sm, xl, w, wt, KF + 1, KT);
-        if (KF + 2 < KT) big_step<MT, NT, S, 2>(acc, sm, xl, w, wt, KF + 2, KT);
-    }
+    for (int kb = 0; kb < KF; kb += S) big_group<NT, S, 0>(acc, sm, xl, w, wt, a0, kb, KT);
+    if (KF < KT) big_step<NT, S, 0>(acc, sm, xl, w, wt, a0, KF, KT);
+    if (KF + 1 < KT) big_step<NT, S, 1>(acc, sm, xl, w, wt, a0, KF + 1, KT);
+    if constexpr (S > 3)
+        if (KF + 2 < KT) big_step<NT, S, 2>(acc, sm, xl, w, wt, a0, KF + 2, KT);
 }
 
-// Loads the item's row scales and the block's weight-tile scales into LDS
-// (2^0 where the operand has none).  row_scale_base(r) gives row r's scale
-// row; tile_scale_base(t) tile t's (t = 2*wave + 0/1).
-template <int MT, class RowF, class TileF>
-__device__ __forceinline__ void big_load_scales(BigSmem<MT>& sm, int KT, bool has_x, bool has_w,
-                                                RowF row_scale_base, TileF tile_scale_base) {
-    for (int i = threadIdx.x; i < MT * 16 * KT; i += kBigThreads) {
-        const int r = i / KT, k = i - r * KT;
-        sm.sfx[r][k] = has_x ? row_scale_base(r)[k] : (uint8_t)127;
-    }
-    for (int i = threadIdx.x; i < 16 * KT; i += kBigThreads) {
-        const int t = i / KT, k = i - t * KT;
-        sm.sfw[t][k] = has_w ? tile_scale_base(t)[k] : (uint8_t)127;
-    }
-    __syncthreads();
-}
-
-// Per-item context shared by the two kernels.
+// Per-unit context shared by the two kernels.
 struct BigItem {
-    int e, m0, rows, off, ntiles;
+    int e, m0, rows, off, bx;
 };
 
-__device__ __forceinline__ bool big_item(const GemmParams& p, BigItem& it) {
-    const int item = blockIdx.y;
-    if (item >= p.status[1]) return false;
+// Work unit u = item * nb + bx.  The XCDs take workgroups round-robin, so
+// workgroup L (the k-th of XCD L%8, k = L/8) runs unit (L%8)*c + k with
+// c = ceil(units / 8): each XCD walks a contiguous range.  The grid has
+// nb * max_items + 8 workgroups, enough for 8*c; the surplus exits.
+__device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& it) {
+    const int units = nb * p.status[1];
+    const int c = (units + 7) >> 3;
+    const int L = blockIdx.x;
+    const int k = L >> 3;
+    const int u = (L & 7) * c + k;
+    if (k >= c || u >= units) return false;
+    const int item = u / nb;
+    it.bx = u - item * nb;
     const int4 v = reinterpret_cast<const int4*>(p.items)[item];
     it.e = v.x;
     it.m0 = v.y;
     it.rows = v.z - v.y;
     it.off = p.offsets[it.e];
-    it.ntiles = (it.rows + 15) >> 4;
     return true;
 }
 
-template <int NT>
-__device__ __forceinline__ void zero2(v4f (&acc)[2][NT]) {
+// Stages the item's row scales ([k-step][row], 2^0 without x_sf) and the
+// block's 16 weight-tile scales ([k-step][tile], 2^0 without w_sf) in LDS.
+// row_scale(r) points at row r's KT scale bytes; tile_scale(t) at tile t's.
+template <class RowF, class TileF>
+__device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, bool has_x,
+                                                bool has_w, RowF row_scale, TileF tile_scale) {
+    for (int r = threadIdx.x; r < nrows; r += kBigThreads) {
+        if (has_x) {
+            const uint8_t* src = row_scale(r);
+            for (int k = 0; k < KT; ++k) sm.sfx[k][r] = src[k];
+        } else {
+            for (int k = 0; k < KT; ++k) sm.sfx[k][r] = 127;
+        }
+    }
+    for (int i = threadIdx.x; i < 4 * kWT * KT; i += kBigThreads) {
+        const int t = i & (4 * kWT - 1), k = i >> 4;
+        sm.sfw[k][t] = has_w ? tile_scale(t)[k] : (uint8_t)127;
+    }
+    __syncthreads();
+}
+
+// NT as run for an item of `tiles` (<= kBigMaxTiles) token tiles: exact up
+// to 8, then even.  (NT >= 14 does not fit the register file: it spills.)
+#define MM_BIG_DISPATCH(BODY)             \
+    switch (tiles) {                      \
+        case 1: BODY(1); break;           \
+        case 2: BODY(2); break;           \
+        case 3: BODY(3); break;           \
+        case 4: BODY(4); break;           \
+        case 5: BODY(5); break;           \
+        case 6: BODY(6); break;           \
+        case 7: BODY(7); break;           \
+        case 8: BODY(8); break;           \
+        case 9: case 10: BODY(10); break; \
+        default: BODY(12); break;         \
+    }
+
+// Sets the loader's row offsets: row r of the item (r >= rows: row 0,
+// whose bytes are loaded but whose results are never stored).
+template <int NT, class RowOff>
+__device__ __forceinline__ void big_loader_init(XLoader<NT>& xl, RowOff row_off) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < XLoader<NT>::U; ++u) {
+        const int i = XLoader<NT>::chunk(u);
+        xl.off[u] = row_off(XLoader<NT>::row_of(i)) + XLoader<NT>::cc_of(i) * 16;
+    }
 }
 
 // ---------------------------------------------------------------------- L1 --
-template <int MT, int NT>
-__device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it,
-                                            BigSmem<MT>& sm, XLoader<MT>& xl) {
+template <int NT>
+__device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, G = p.G, KT = H >> 7;
-    const int hw = blockIdx.x * kL1BlockH + wave * 16;   // this wave's hidden columns
+    XLoader<NT> xl;
+    xl.base = p.x;
+    big_loader_init<NT>(xl, [&](int r) {
+        const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
+        return (p.perm[slot] / (uint32_t)p.topk) * (uint32_t)H;
+    });
+    // this wave's 32 hidden columns: gate tiles ntg, ntg+1 and up tiles ntu, ntu+1
+    const int hw = it.bx * kL1BlockH + wave * 32;
     const int rho = (hw / G) * 2 * G + (hw % G);
     const int ntg = rho >> 4, ntu = ntg + (G >> 4);
     const uint8_t* we = p.w + (size_t)it.e * (size_t)(2 * I) * H;
     const size_t tstride = (size_t)KT * kTileBytes;
-    const uint8_t* wt[2] = {we + (size_t)ntg * tstride + lane * 16,
-                            we + (size_t)ntu * tstride + lane * 16};
-    v4f acc[2][NT];
-    zero2<NT>(acc);
-    big_mainloop<MT, NT>(acc, sm, xl, wt, KT);
+    const uint8_t* wt[kWT] = {we + (size_t)ntg * tstride + lane * 16,
+                              we + (size_t)(ntg + 1) * tstride + lane * 16,
+                              we + (size_t)ntu * tstride + lane * 16,
+                              we + (size_t)(ntu + 1) * tstride + lane * 16};
+    v4f acc[kWT][NT];
+    big_mainloop<NT>(acc, sm, xl, wt, KT);
 
-    // h = silu(g) * u: channels hw + 4*(L/16) + i, token 16*j + L%16
-    float hv[NT][4];
+    // h = silu(g) * u: channels hw + 16*t + 4*(L/16) + i, token 16*j + L%16
+    float hv[2][NT][4];
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float g = acc[0][j][i], u = acc[1][j][i];
-            hv[j][i] = (g / (1.0f + __expf(-g))) * u;
-        }
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float g = acc[t][j][i], u = acc[t + 2][j][i];
+                hv[t][j][i] = (g / (1.0f + __expf(-g))) * u;
+            }
     const int I128 = I >> 7;
+    float inv[NT];
     if (p.ffn_ue8m0) {
-        // amax over the block's 128 hidden columns = the 8 waves; the LDS
+        // amax over the block's 128 hidden columns = the 4 waves; the LDS
         // tiles are free after the main loop's last barrier.
-        float* red = reinterpret_cast<float*>(&sm.x[0][0]);   // [8][MT*16]
+        float* red = reinterpret_cast<float*>(&sm.x[0][0]);   // [4][kBigRows]
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            float m = fmaxf(fmaxf(fabsf(hv[j][0]), fabsf(hv[j][1])),
-                            fmaxf(fabsf(hv[j][2]), fabsf(hv[j][3])));
+            float m = 0.f;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(hv[t][j][i]));
             m = fmaxf(m, __shfl_xor(m, 16, 64));
             m = fmaxf(m, __shfl_xor(m, 32, 64));
-            if (lane < 16) red[wave * (MT * 16) + 16 * j + lane] = m;
+            if (lane < 16) red[wave * kBigRows + 16 * j + lane] = m;
         }
         __syncthreads();
 #pragma unroll
@@ -247,147 +377,108 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
             const int r = 16 * j + (lane & 15);
             float amax = red[r];
 #pragma unroll
-            for (int w = 1; w < 8; ++w) amax = fmaxf(amax, red[w * (MT * 16) + r]);
+            for (int w = 1; w < 4; ++w) amax = fmaxf(amax, red[w * kBigRows + r]);
             const uint32_t sb = block_scale_byte(amax);
-            const float inv = inv_scale(sb);
-            if (r < it.rows) {
-                const size_t slot = (size_t)(it.off + it.m0 + r);
-                *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 4 * (lane >> 4)) =
-                    pack4_fp8(hv[j][0] * inv, hv[j][1] * inv, hv[j][2] * inv, hv[j][3] * inv);
-                if (wave == 0 && lane < 16) p.out_sf[slot * I128 + blockIdx.x] = (uint8_t)sb;
-            }
+            inv[j] = inv_scale(sb);
+            if (wave == 0 && lane < 16 && r < it.rows)
+                p.out_sf[(size_t)(it.off + it.m0 + r) * I128 + it.bx] = (uint8_t)sb;
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const int r = 16 * j + (lane & 15);
-            if (r < it.rows) {
-                const size_t slot = (size_t)(it.off + it.m0 + r);
-                *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 4 * (lane >> 4)) =
-                    pack4_fp8(hv[j][0], hv[j][1], hv[j][2], hv[j][3]);
-            }
+        for (int j = 0; j < NT; ++j) inv[j] = 1.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int r = 16 * j + (lane & 15);
+        if (r < it.rows) {
+            uint8_t* dst = p.out8 + (size_t)(it.off + it.m0 + r) * I + hw + 4 * (lane >> 4);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                *reinterpret_cast<uint32_t*>(dst + 16 * t) =
+                    pack4_fp8(hv[t][j][0] * inv[j], hv[t][j][1] * inv[j], hv[t][j][2] * inv[j],
+                              hv[t][j][3] * inv[j]);
         }
     }
 }
 
 // NT (the item's token tiles) is uniform over the block, so every wave runs
 // the same body and the same barriers.
-template <int MT>
 __global__ void __launch_bounds__(kBigThreads) l1_big_kernel(GemmParams p) {
-    __shared__ BigSmem<MT> sm;
+    __shared__ BigSmem sm;
     BigItem it;
-    if (!big_item(p, it)) return;
-    XLoader<MT> xl;
-    xl.base = p.x;
-    const int KT = p.H >> 7;
-#pragma unroll
-    for (int u = 0; u < XLoader<MT>::U; ++u) {
-        const int i = threadIdx.x + kBigThreads * u;
-        const int r = XLoader<MT>::row_of(i), cc = XLoader<MT>::cc_of(i);
-        const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
-        const uint32_t tok = p.perm[slot] / (uint32_t)p.topk;
-        xl.off[u] = tok * (uint32_t)p.H + cc * 16;
-    }
-    {
-        // scales: x rows through perm[]; W1 tiles 2*wave (gate), 2*wave+1 (up)
-        const int I = p.I, G = p.G;
-        big_load_scales<MT>(
-            sm, KT, p.x_sf != nullptr, p.w_sf != nullptr,
-            [&](int r) {
-                const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
-                return p.x_sf + (size_t)(p.perm[slot] / (uint32_t)p.topk) * KT;
-            },
-            [&](int t) {
-                const int hw = blockIdx.x * kL1BlockH + (t >> 1) * 16;
-                const int rho = (hw / G) * 2 * G + (hw % G) + ((t & 1) ? G : 0);
-                return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
-            });
-    }
-    switch (it.ntiles) {
-        case 1: l1_big_body<MT, 1>(p, it, sm, xl); break;
-        case 2: l1_big_body<MT, 2>(p, it, sm, xl); break;
-        case 3: l1_big_body<MT, 3>(p, it, sm, xl); break;
-        case 4: l1_big_body<MT, 4>(p, it, sm, xl); break;
-        case 5: if constexpr (MT >= 5) l1_big_body<MT, 5>(p, it, sm, xl); break;
-        case 6: if constexpr (MT >= 6) l1_big_body<MT, 6>(p, it, sm, xl); break;
-        case 7: if constexpr (MT >= 7) l1_big_body<MT, 7>(p, it, sm, xl); break;
-        default: if constexpr (MT >= 8) l1_big_body<MT, 8>(p, it, sm, xl); break;
-    }
+    if (!big_unit(p, p.I / kL1BlockH, it)) return;
+    const int KT = p.H >> 7, I = p.I, G = p.G;
+    const int tiles = (it.rows + 15) >> 4;
+    // scales: x rows through perm[]; W1 tiles 4*wave + {gate, gate, up, up}
+    big_load_scales(
+        sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
+        [&](int r) {
+            const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
+            return p.x_sf + (size_t)(p.perm[slot] / (uint32_t)p.topk) * KT;
+        },
+        [&](int t) {
+            const int hw = it.bx * kL1BlockH + (t >> 2) * 32;
+            const int rho = (hw / G) * 2 * G + (hw % G) + ((t & 2) ? G : 0);
+            return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
+        });
+#define MM_L1_BODY(n) l1_big_body<n>(p, it, sm)
+    MM_BIG_DISPATCH(MM_L1_BODY)
+#undef MM_L1_BODY
 }
 
 // ---------------------------------------------------------------------- L2 --
-template <int MT, int NT>
-__device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& it,
-                                            BigSmem<MT>& sm, XLoader<MT>& xl) {
+template <int NT>
+__device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, KT = I >> 7;
-    const int n0 = blockIdx.x * kL2BlockN + wave * 32;
+    XLoader<NT> xl;
+    xl.base = p.x;
+    big_loader_init<NT>(xl, [&](int r) {
+        return (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
+    });
+    const int n0 = it.bx * kL2BlockN + wave * 64;   // this wave's 64 output channels
     const uint8_t* we = p.w + (size_t)it.e * (size_t)H * I;
     const size_t tstride = (size_t)KT * kTileBytes;
-    const uint8_t* wt[2] = {we + (size_t)(n0 >> 4) * tstride + lane * 16,
-                            we + (size_t)((n0 >> 4) + 1) * tstride + lane * 16};
-    v4f acc[2][NT];
-    zero2<NT>(acc);
-    big_mainloop<MT, NT>(acc, sm, xl, wt, KT);
+    const uint8_t* wt[kWT];
+#pragma unroll
+    for (int t = 0; t < kWT; ++t) wt[t] = we + (size_t)((n0 >> 4) + t) * tstride + lane * 16;
+    v4f acc[kWT][NT];
+    big_mainloop<NT>(acc, sm, xl, wt, KT);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         const int r = 16 * j + (lane & 15);
         if (r < it.rows) {
-            const size_t slot = (size_t)(it.off + it.m0 + r);
+            uint16_t* dst = p.out16 + (size_t)(it.off + it.m0 + r) * H + n0 + 4 * (lane >> 4);
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < kWT; ++t) {
                 uint2 v;
                 v.x = bf16_rne(acc[t][j][0]) | (bf16_rne(acc[t][j][1]) << 16);
                 v.y = bf16_rne(acc[t][j][2]) | (bf16_rne(acc[t][j][3]) << 16);
-                *reinterpret_cast<uint2*>(p.out16 + slot * H + n0 + 16 * t + 4 * (lane >> 4)) = v;
+                *reinterpret_cast<uint2*>(dst + 16 * t) = v;
             }
         }
     }
 }
 
-template <int MT>
 __global__ void __launch_bounds__(kBigThreads) l2_big_kernel(GemmParams p) {
-    __shared__ BigSmem<MT> sm;
+    __shared__ BigSmem sm;
     BigItem it;
-    if (!big_item(p, it)) return;
-    XLoader<MT> xl;
-    xl.base = p.x;
-    const int KT = p.I >> 7;
-#pragma unroll
-    for (int u = 0; u < XLoader<MT>::U; ++u) {
-        const int i = threadIdx.x + kBigThreads * u;
-        const int r = XLoader<MT>::row_of(i), cc = XLoader<MT>::cc_of(i);
-        const uint32_t slot = (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0));
-        xl.off[u] = slot * (uint32_t)p.I + cc * 16;
-    }
-    {
-        // scales: ffn rows in slot order; W2 tiles of this block's 256 channels
-        const int H = p.H;
-        big_load_scales<MT>(
-            sm, KT, p.x_sf != nullptr, p.w_sf != nullptr,
-            [&](int r) {
-                return p.x_sf + (size_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * KT;
-            },
-            [&](int t) {
-                const int n = blockIdx.x * kL2BlockN + t * 16;
-                return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
-            });
-    }
-    switch (it.ntiles) {
-        case 1: l2_big_body<MT, 1>(p, it, sm, xl); break;
-        case 2: l2_big_body<MT, 2>(p, it, sm, xl); break;
-        case 3: l2_big_body<MT, 3>(p, it, sm, xl); break;
-        case 4: l2_big_body<MT, 4>(p, it, sm, xl); break;
-        case 5: if constexpr (MT >= 5) l2_big_body<MT, 5>(p, it, sm, xl); break;
-        case 6: if constexpr (MT >= 6) l2_big_body<MT, 6>(p, it, sm, xl); break;
-        case 7: if constexpr (MT >= 7) l2_big_body<MT, 7>(p, it, sm, xl); break;
-        default: if constexpr (MT >= 8) l2_big_body<MT, 8>(p, it, sm, xl); break;
-    }
+    if (!big_unit(p, p.H / kL2BlockN, it)) return;
+    const int KT = p.I >> 7, H = p.H;
+    const int tiles = (it.rows + 15) >> 4;
+    // scales: ffn rows in slot order; W2 tiles of this block's 256 channels
+    big_load_scales(
+        sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
+        [&](int r) { return p.x_sf + (size_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * KT; },
+        [&](int t) {
+            const int n = it.bx * kL2BlockN + t * 16;
+            return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
+        });
+#define MM_L2_BODY(n) l2_big_body<n>(p, it, sm)
+    MM_BIG_DISPATCH(MM_L2_BODY)
+#undef MM_L2_BODY
 }
 
-template __global__ void l1_big_kernel<4>(GemmParams);
-template __global__ void l1_big_kernel<8>(GemmParams);
-template __global__ void l2_big_kernel<4>(GemmParams);
-template __global__ void l2_big_kernel<8>(GemmParams);
+#undef MM_BIG_DISPATCH
 
 }  // namespace mm

@@ -22,12 +22,13 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 int auto_m_tile(int tokens, int topk, int E) {
     // Rows per work item: one item per expert when the expected expert load
     // (plus the spread of a random router) fits, so that each expert's weights
-    // stream from HBM once.  <= 32 rows: decode-shaped kernels; 64..256: the
-    // 8-wave LDS-staged kernels.
+    // stream from HBM once.  <= 32 rows: decode-shaped kernels; 64..192: the
+    // LDS-staged kernels (up to 12 token tiles per item).
     const double mean = (double)tokens * topk / (E > 0 ? E : 1);
     if (mean <= 20.0) return 32;
     if (mean <= 44.0) return 64;
-    return 128;
+    if (mean <= 96.0) return 128;
+    return 16 * mm::kBigMaxTiles;
 }
 
 int pairing_block(int I) { return I < 256 ? I : 256; }
@@ -37,7 +38,8 @@ int check_dims(int topk, int E, int H, int I, int win_cap) {
     if (H < 256 || H % 256 != 0 || I < 128 || I % 128 != 0) return kErrBadDims;
     if (H > 128 * mm::kBigMaxKT || I > 128 * mm::kBigMaxKT) return kErrBadDims;
     if (I % pairing_block(I) != 0) return kErrBadDims;
-    if (win_cap != 0 && win_cap != 16 && win_cap != 32 && win_cap != 64 && win_cap != 128)
+    if (win_cap != 0 && win_cap != 16 && win_cap != 32 && win_cap != 64 && win_cap != 128 &&
+        win_cap != 16 * mm::kBigMaxTiles)
         return kErrBadDims;
     return kOk;
 }
@@ -135,24 +137,21 @@ mm::GemmParams gemm_params(const MegaLaunchArgs& a, const Bound& b) {
 
 using GemmKernel = void (*)(mm::GemmParams);
 
-// Decode-shaped (4 waves, MT = 1, 2) for m_tile <= 32; LDS-staged 8-wave
-// kernels (MT = 4, 8) above.
-void launch_gemm(const GemmKernel (&small)[2], const GemmKernel (&big)[2], int m_tile,
-                 int nblocks_small, int nblocks_big, int max_items, hipStream_t s,
-                 const mm::GemmParams& p) {
+// Decode-shaped kernels (MT = 1, 2) for m_tile <= 32; above, the LDS-staged
+// kernels on a 1-D grid of nb * max_items + 8 workgroups (the kernel maps
+// workgroups to (item, block) units XCD by XCD and drops the surplus).
+void launch_gemm(const GemmKernel (&small)[2], GemmKernel big, int m_tile, int nb,
+                 int max_items, hipStream_t s, const mm::GemmParams& p) {
     if (m_tile <= 32) {
-        hipLaunchKernelGGL(small[m_tile <= 16 ? 0 : 1], dim3(nblocks_small, max_items),
+        hipLaunchKernelGGL(small[m_tile <= 16 ? 0 : 1], dim3(nb, max_items),
                            dim3(mm::kGemmThreads), 0, s, p);
     } else {
-        const int i = m_tile <= 64 ? 0 : 1;
-        hipLaunchKernelGGL(big[i], dim3(nblocks_big, max_items), dim3(mm::kBigThreads), 0, s, p);
+        hipLaunchKernelGGL(big, dim3(nb * max_items + 8), dim3(mm::kBigThreads), 0, s, p);
     }
 }
 
 const GemmKernel kL1Small[2] = {mm::l1_kernel<1>, mm::l1_kernel<2>};
-const GemmKernel kL1Big[2] = {mm::l1_big_kernel<4>, mm::l1_big_kernel<8>};
 const GemmKernel kL2Small[2] = {mm::l2_kernel<1>, mm::l2_kernel<2>};
-const GemmKernel kL2Big[2] = {mm::l2_big_kernel<4>, mm::l2_big_kernel<8>};
 
 int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     Bound b;
@@ -167,7 +166,7 @@ int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     p.out8 = b.ws + b.L.ffn;
     p.out_sf = b.ws + b.L.ffn_sf;
     const int nb = a.intermediate / mm::kL1BlockH;
-    launch_gemm(kL1Small, kL1Big, b.m_tile, nb, nb, b.L.max_items, s, p);
+    launch_gemm(kL1Small, mm::l1_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
 }
 
@@ -183,7 +182,7 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     p.w_sf = a.w2_sf;
     p.out16 = at<uint16_t>(b, b.L.l2);
     const int nb = a.hidden / mm::kL2BlockN;
-    launch_gemm(kL2Small, kL2Big, b.m_tile, nb, nb, b.L.max_items, s, p);
+    launch_gemm(kL2Small, mm::l2_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
 }
 
@@ -343,12 +342,10 @@ void dump_kernel_resources() {
     print_attr("route_scatter", (const void*)mm::route_scatter_kernel);
     print_attr("l1_kernel<1>", (const void*)mm::l1_kernel<1>);
     print_attr("l1_kernel<2>", (const void*)mm::l1_kernel<2>);
-    print_attr("l1_big_kernel<4>", (const void*)mm::l1_big_kernel<4>);
-    print_attr("l1_big_kernel<8>", (const void*)mm::l1_big_kernel<8>);
+    print_attr("l1_big_kernel", (const void*)mm::l1_big_kernel);
     print_attr("l2_kernel<1>", (const void*)mm::l2_kernel<1>);
     print_attr("l2_kernel<2>", (const void*)mm::l2_kernel<2>);
-    print_attr("l2_big_kernel<4>", (const void*)mm::l2_big_kernel<4>);
-    print_attr("l2_big_kernel<8>", (const void*)mm::l2_big_kernel<8>);
+    print_attr("l2_big_kernel", (const void*)mm::l2_big_kernel);
     print_attr("combine", (const void*)mm::combine_kernel);
     std::fflush(stdout);
 }

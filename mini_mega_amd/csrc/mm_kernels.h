@@ -13,7 +13,8 @@ constexpr int kRouteThreads = 256;
 constexpr int kRouteChunk = 1024;   // pairs per routing chunk
 
 constexpr int kGemmThreads = 256;   // 4 waves per workgroup (decode-shaped GEMMs)
-constexpr int kBigThreads = 512;    // 8 waves per workgroup (large-M GEMMs)
+constexpr int kBigThreads = 256;    // 4 waves per workgroup, one per SIMD (large-M GEMMs)
+constexpr int kBigMaxTiles = 12;    // large-M GEMMs: up to 12 token tiles (192 rows) per item
 constexpr int kBigMaxKT = 64;       // large-M GEMMs: K / 128 <= 64 (H, I <= 8192)
 constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 workgroup
 constexpr int kL2BlockN = 256;      // output channels per L2 workgroup
@@ -37,15 +38,10 @@ struct GemmParams {
     int ffn_ue8m0;
 };
 
-// Scale byte 127 (2^0) read with stride 0 when an operand carries no scales,
-// so scale loads are unconditional (no branch in the k loops).
-__device__ const uint8_t kUnitScale[16] = {127, 127, 127, 127, 127, 127, 127, 127,
-                                          127, 127, 127, 127, 127, 127, 127, 127};
-
 template <int MT> __global__ void l1_kernel(GemmParams p);
 template <int MT> __global__ void l2_kernel(GemmParams p);
-template <int MT> __global__ void l1_big_kernel(GemmParams p);
-template <int MT> __global__ void l2_big_kernel(GemmParams p);
+__global__ void l1_big_kernel(GemmParams p);
+__global__ void l2_big_kernel(GemmParams p);
 
 __global__ void route_hist_kernel(const int64_t*, int, int, int*);
 __global__ void route_scan_kernel(int*, int, int, int, int, int, int*, int*, int*, int*);
