@@ -59,7 +59,7 @@ struct MegaLaunchArgs {
     int R = 1, rank = 0;         // single GPU: R = 1, rank = 0
     int tokens = 0;              // tokens in this launch
     int slot_capacity = 0;       // per-expert slot cap; 0 = no cap (tokens*topk)
-    int win_cap = 0;             // max rows per work item: 0 (auto), 16, 32, 64, 128, 192
+    int win_cap = 0;             // max rows per work item: 0 (auto), 16, 32, 64, 128, 256
     int grid = 0, threads = 0;   // informational (filled by make_args)
     int64_t smem = 0;
 

@@ -1,30 +1,30 @@
 // gemm_big.hip -- the L1 / L2 grouped GEMMs for large per-expert row counts
-// (work items of 33..192 token rows: T >= ~1024 and skewed routing), where
+// (work items of 33..256 token rows: T >= ~1024 and skewed routing), where
 // the decode-shaped kernels of gemm.hip would re-stream each expert's weights
 // once per 32 rows.
 //
 // Reference counterparts: r24_l1_big / r24_l2_big (src/compute_big.cuh:888-1161,
 // 1375-1679), the reference's count-tiered big-window GEMMs.
 //
-// One 4-wave workgroup (one wave per SIMD) per work unit = (work item, block
-// of 256 weight rows); each wave owns a 64-row weight slice (four 16-row
-// tiles) across all of the item's token rows, so every weight byte is loaded
-// and converted exactly once and every activation operand read from LDS feeds
-// four MFMAs:
-//   * per 128-k step, the 256 threads gather the item's active token rows
+// One 8-wave workgroup (two waves per SIMD) per work unit = (work item,
+// block of 256 weight rows); each wave owns a 32-row weight slice (two
+// 16-row tiles) across all of the item's token rows (up to 256, so that at
+// T = 8192 one item covers an expert and its weights stream from HBM once):
+//   * per 128-k step, the 512 threads gather the item's active token rows
 //     (through perm[] for L1, slot order for L2), convert them once to bf16
 //     with the row's UE8M0 scale folded in (exact), and store them in a
 //     double-buffered LDS tile: [token tile][k-group q][lane][8 bf16], so that
-//     a wave's operand read for one MFMA is 1 KiB contiguous;
-//   * each wave streams its four weight tiles (L1: gate and up rows of 32
-//     hidden columns; L2: 64 output channels) from HBM through a 3- or
+//     a wave's operand read for one MFMA pair is 1 KiB contiguous (the LDS
+//     reads then run at ~2/3 of the measured ~190 B/clk/CU at full MFMA rate);
+//   * each wave streams its two weight tiles (L1: gate and up rows of 16
+//     hidden columns; L2: 32 output channels) from HBM through a 3- or
 //     4-stage register pipeline and converts them exactly to bf16;
 //   * v_mfma_f32_16x16x32_bf16 (fp32-accurate sums; see gemm.hip) over the
 //     item's NT active token tiles -- NT is a compile-time specialisation
-//     picked per item (1..8, then even up to 12), so the k loop has no branch
-//     and the 4*NT accumulators (up to 192 registers) are independent chains;
+//     picked per item (1..8, then even up to 16), so the k loop has no branch
+//     and the 2*NT accumulators (up to 128 registers) are independent chains;
 //   * epilogues as in gemm.hip: L1 SwiGLU + fp8 (raw, or per-128 UE8M0 with
-//     the 128-column amax reduced over the 4 waves in LDS), L2 bf16.
+//     the 128-column amax reduced over the 8 waves in LDS), L2 bf16.
 // Work units are numbered so that each XCD runs a contiguous range of them:
 // the N-blocks of one item share that XCD's L2 for the item's activations.
 #include "mm_kernels.h"
@@ -32,61 +32,65 @@
 namespace mm {
 
 constexpr int kXTileBytes = 16 * kTileK * 2;   // one bf16 token tile: 16 rows x 128 k
-constexpr int kWT = 4;                          // weight tiles per wave
+constexpr int kWaves = kBigThreads / 64;        // 8
+constexpr int kWT = 2;                          // weight tiles per wave
+constexpr int kBlockTiles = kWaves * kWT;       // 16 weight tiles = 256 rows per workgroup
 constexpr int kBigRows = kBigMaxTiles * 16;     // token rows per work item (max)
 
 struct alignas(16) BigSmem {
     uint8_t x[2][kBigMaxTiles * kXTileBytes];   // bf16 tiles, double buffered
     uint8_t sfx[kBigMaxKT][kBigRows];           // the item's row scales [k-step][row]
-    uint8_t sfw[kBigMaxKT][4 * kWT];            // the block's 16 weight tiles' scales
+    uint8_t sfw[kBigMaxKT][kBlockTiles];        // the block's weight-tile scales [k-step][tile]
 };
 
-// Loader for NT active token tiles: chunk i = tid + 256*u is row
-// r = 16*(i/128) + i%16 of the item, fp8 bytes [16*cc, 16*cc+16) of the
+// Loader for NT active token tiles: chunk i = (tid + 512*u) mod (NT*128) is
+// row r = 16*(i/128) + i%16 of the item, fp8 bytes [16*cc, 16*cc+16) of the
 // k-step with cc = (i/16)%8: k-group g = cc/2, MFMA groups q = 2*(cc%2) and
 // q+1.  Rows vary fastest, so the 16 lanes of an LDS write phase fill 16
-// consecutive 16-byte slots (no bank conflicts).  For odd NT the upper half
-// of the last round re-does the chunk 128 below it (same bytes to the same
-// LDS slot), which keeps every thread's work uniform.  XS register stages:
-// with two (NT <= 8), the rows of k-step kt+2 are in flight while kt+1 is
-// written to LDS; with one (larger NT: registers go to accumulators, and a
-// k-step's MFMAs alone cover an L2 hit), kt+1 is loaded during step kt.
+// consecutive 16-byte slots (no bank conflicts).  When NT*128 is not a
+// multiple of 512 some threads redo another thread's chunk (same bytes to
+// the same LDS slot), which keeps every thread's work uniform.  XS register
+// stages: with two (NT <= 12), the rows of k-step kt+2 are in flight while
+// kt+1 is written to LDS; with one (larger NT: registers go to accumulators,
+// and a k-step's MFMAs alone cover an L2 hit), kt+1 is loaded during kt.
 template <int NT>
 struct XLoader {
     static constexpr int U = (NT * 128 + kBigThreads - 1) / kBigThreads;
-    static constexpr int XS = NT > 8 ? 1 : 2;
+    static constexpr int XS = NT > 12 ? 1 : 2;
     const uint8_t* base;
     uint32_t off[U];
     v4i reg[XS][U];
 
     __device__ __forceinline__ static int chunk(int u) {
-        const int i = threadIdx.x + kBigThreads * u;
-        return i < NT * 128 ? i : i - 128;
+        return (threadIdx.x + kBigThreads * u) % (NT * 128);
     }
     __device__ __forceinline__ static int row_of(int i) { return ((i >> 7) << 4) | (i & 15); }
     __device__ __forceinline__ static int cc_of(int i) { return (i >> 4) & 7; }
+    __device__ __forceinline__ static int slot_of(int i) {
+        const int r = row_of(i), cc = cc_of(i);
+        return (r >> 4) * kXTileBytes + 2 * (cc & 1) * 1024 + ((r & 15) + 16 * (cc >> 1)) * 16;
+    }
 
     __device__ __forceinline__ void issue(int kt, int rs) {
 #pragma unroll
         for (int u = 0; u < U; ++u) reg[rs][u] = load16(base + off[u] + kt * kTileK);
     }
+    // Writes chunk u of register stage rs, scaled by 2^(e - 127), to LDS stage xw.
+    __device__ __forceinline__ void commit_chunk(uint8_t* xw, int rs, int u, uint32_t e) {
+        uint8_t* t = xw + slot_of(chunk(u));
+        const float s = ue8m0_to_f32(e);
+        *reinterpret_cast<v8bf*>(t) = fp8x8_to_bf16(reg[rs][u][0], reg[rs][u][1], s);
+        *reinterpret_cast<v8bf*>(t + 1024) = fp8x8_to_bf16(reg[rs][u][2], reg[rs][u][3], s);
+    }
     __device__ __forceinline__ void commit(BigSmem& sm, int stage, int rs, int kt) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = chunk(u);
-            const int r = row_of(i), cc = cc_of(i);
-            const int lane_slot = (r & 15) + 16 * (cc >> 1);
-            const int q0 = 2 * (cc & 1);
-            uint8_t* t = &sm.x[stage][(r >> 4) * kXTileBytes + q0 * 1024 + lane_slot * 16];
-            const float s = ue8m0_to_f32(sm.sfx[kt][r]);
-            *reinterpret_cast<v8bf*>(t) = fp8x8_to_bf16(reg[rs][u][0], reg[rs][u][1], s);
-            *reinterpret_cast<v8bf*>(t + 1024) = fp8x8_to_bf16(reg[rs][u][2], reg[rs][u][3], s);
-        }
+        for (int u = 0; u < U; ++u)
+            commit_chunk(&sm.x[stage][0], rs, u, sm.sfx[kt][row_of(chunk(u))]);
     }
 };
 
 struct WStage {
-    v4i a[kWT][2];   // four weight tiles, two 16-byte halves each
+    v4i a[kWT][2];   // two weight tiles, two 16-byte halves each
 };
 
 __device__ __forceinline__ void w_load(WStage& w, const uint8_t* const* wt, int kt) {
@@ -103,43 +107,46 @@ __device__ __forceinline__ v8bf w_group(const WStage& w, int t, int q, float s) 
     return fp8x8_to_bf16(w.a[t][q >> 1][2 * (q & 1)], w.a[t][q >> 1][2 * (q & 1) + 1], s);
 }
 
-// The wave's four weight-tile scale bytes of k-step kt (byte t = tile t).
+// The wave's two weight-tile scale bytes of k-step kt (byte t = tile t).
 __device__ __forceinline__ uint32_t w_scales(const BigSmem& sm, int kt) {
     const int wave = threadIdx.x >> 6;
-    return *reinterpret_cast<const uint32_t*>(&sm.sfw[kt][kWT * wave]);
+    return *reinterpret_cast<const uint16_t*>(&sm.sfw[kt][kWT * wave]);
 }
 
 __device__ __forceinline__ float scale_of(uint32_t bytes, int t) {
     return ue8m0_to_f32((bytes >> (8 * t)) & 0xffu);
 }
 
-// Weight register stages: 4 for NT <= 8 (even, so that two activation
-// stages alternate within a group), 3 above (a k-step of >= 160 MFMAs per
-// wave covers the latency of two steps ahead).
+// Weight register stages: 4 for NT <= 12 (even, so that two activation
+// stages alternate within a group), 3 above (registers; a k-step of >= 112
+// MFMA pairs per wave covers the latency of two steps ahead).
 template <int NT>
-constexpr int big_stages() { return NT > 8 ? 3 : 4; }
+constexpr int big_stages() { return NT > 12 ? 3 : 4; }
 
-constexpr int kBigReadAhead = 2;   // activation operand reads in flight ahead of their MFMAs
+// Activation operand reads in flight ahead of their MFMAs: 3, or 2 above
+// NT = 12 (registers).
+template <int NT>
+constexpr int big_read_ahead() { return NT > 12 ? 2 : 3; }
 
 // One k-step, software-pipelined by hand.  The step's 4*NT chunks (k-group
-// q, token tile j) each hold: the LDS read of the activation operand two
+// q, token tile j) each hold: the LDS read of the activation operand D
 // chunks ahead, a share of the conversions of the next k-group's weight
 // operands (in the last group: the next k-step's first), a share of the
-// activation commit of k-step kt+1 (last group only), and the chunk's 4
+// activation commit of k-step kt+1 (last group only), and the chunk's 2
 // MFMAs.  A scheduling fence closes every chunk, so the compiler keeps this
-// order: operand reads stay two chunks ahead of their use, and conversions
-// overlap the MFMAs instead of stalling them.  Before the chunks: the
-// prefetches of activations (kt+XS) and weights (kt+S-1), with indices
-// clamped to the last step (a redundant in-bounds reload keeps the loop free
-// of branches, so the compiler's wait counts stay partial).  After: the
-// barrier that publishes the committed activations.  a0 carries the
-// converted k-group-0 operand from one step to the next.
+// order: operand reads stay ahead of their use, and conversions overlap the
+// MFMAs instead of stalling them.  Before the chunks: the prefetches of
+// activations (kt+XS) and weights (kt+S-1), with indices clamped to the last
+// step (a redundant in-bounds reload keeps the loop free of branches, so the
+// compiler's wait counts stay partial).  After: the barrier that publishes
+// the committed activations.  a0 carries the converted k-group-0 operand from
+// one step to the next.
 template <int NT, int S, int s>
 __device__ __forceinline__ void big_step(v4f (&acc)[kWT][NT], BigSmem& sm, XLoader<NT>& xl,
                                          WStage (&w)[S], const uint8_t* const* wt,
                                          v8bf (&a0)[kWT], int kt, int KT) {
     constexpr int XS = XLoader<NT>::XS, U = XLoader<NT>::U;
-    constexpr int G = 4 * NT, D = kBigReadAhead;
+    constexpr int G = 4 * NT, D = big_read_ahead<NT>() < G ? big_read_ahead<NT>() : G;
     constexpr int rs = XS == 2 ? ((s + 1) & 1) : 0;   // register stage holding k-step kt+1
     const int lane = threadIdx.x & 63;
     xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
@@ -176,17 +183,7 @@ __device__ __forceinline__ void big_step(v4f (&acc)[kWT][NT], BigSmem& sm, XLoad
         if (q == 3) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                if (j == (u * NT) / U) {
-                    const int i = XLoader<NT>::chunk(u);
-                    const int r = XLoader<NT>::row_of(i), cc = XLoader<NT>::cc_of(i);
-                    uint8_t* t = xw + (r >> 4) * kXTileBytes + 2 * (cc & 1) * 1024 +
-                                 ((r & 15) + 16 * (cc >> 1)) * 16;
-                    const float sx = ue8m0_to_f32(xs[u]);
-                    *reinterpret_cast<v8bf*>(t) =
-                        fp8x8_to_bf16(xl.reg[rs][u][0], xl.reg[rs][u][1], sx);
-                    *reinterpret_cast<v8bf*>(t + 1024) =
-                        fp8x8_to_bf16(xl.reg[rs][u][2], xl.reg[rs][u][3], sx);
-                }
+                if (j == (u * NT) / U) xl.commit_chunk(xw, rs, u, xs[u]);
         }
 #pragma unroll
         for (int t = 0; t < kWT; ++t) acc[t][j] = mfma_bf16(ac[t], b[g % (D + 1)], acc[t][j]);
@@ -285,27 +282,29 @@ __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, 
             for (int k = 0; k < KT; ++k) sm.sfx[k][r] = 127;
         }
     }
-    for (int i = threadIdx.x; i < 4 * kWT * KT; i += kBigThreads) {
-        const int t = i & (4 * kWT - 1), k = i >> 4;
+    for (int i = threadIdx.x; i < kBlockTiles * KT; i += kBigThreads) {
+        const int t = i % kBlockTiles, k = i / kBlockTiles;
         sm.sfw[k][t] = has_w ? tile_scale(t)[k] : (uint8_t)127;
     }
     __syncthreads();
 }
 
 // NT as run for an item of `tiles` (<= kBigMaxTiles) token tiles: exact up
-// to 8, then even.  (NT >= 14 does not fit the register file: it spills.)
-#define MM_BIG_DISPATCH(BODY)             \
-    switch (tiles) {                      \
-        case 1: BODY(1); break;           \
-        case 2: BODY(2); break;           \
-        case 3: BODY(3); break;           \
-        case 4: BODY(4); break;           \
-        case 5: BODY(5); break;           \
-        case 6: BODY(6); break;           \
-        case 7: BODY(7); break;           \
-        case 8: BODY(8); break;           \
-        case 9: case 10: BODY(10); break; \
-        default: BODY(12); break;         \
+// to 8, then even.
+#define MM_BIG_DISPATCH(BODY)              \
+    switch (tiles) {                       \
+        case 1: BODY(1); break;            \
+        case 2: BODY(2); break;            \
+        case 3: BODY(3); break;            \
+        case 4: BODY(4); break;            \
+        case 5: BODY(5); break;            \
+        case 6: BODY(6); break;            \
+        case 7: BODY(7); break;            \
+        case 8: BODY(8); break;            \
+        case 9: case 10: BODY(10); break;  \
+        case 11: case 12: BODY(12); break; \
+        case 13: case 14: BODY(14); break; \
+        default: BODY(16); break;          \
     }
 
 // Sets the loader's row offsets: row r of the item (r >= rows: row 0,
@@ -330,43 +329,35 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
         const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
         return (p.perm[slot] / (uint32_t)p.topk) * (uint32_t)H;
     });
-    // this wave's 32 hidden columns: gate tiles ntg, ntg+1 and up tiles ntu, ntu+1
-    const int hw = it.bx * kL1BlockH + wave * 32;
+    // this wave's 16 hidden columns: gate tile ntg, up tile ntu
+    const int hw = it.bx * kL1BlockH + wave * 16;
     const int rho = (hw / G) * 2 * G + (hw % G);
     const int ntg = rho >> 4, ntu = ntg + (G >> 4);
     const uint8_t* we = p.w + (size_t)it.e * (size_t)(2 * I) * H;
     const size_t tstride = (size_t)KT * kTileBytes;
     const uint8_t* wt[kWT] = {we + (size_t)ntg * tstride + lane * 16,
-                              we + (size_t)(ntg + 1) * tstride + lane * 16,
-                              we + (size_t)ntu * tstride + lane * 16,
-                              we + (size_t)(ntu + 1) * tstride + lane * 16};
+                              we + (size_t)ntu * tstride + lane * 16};
     v4f acc[kWT][NT];
     big_mainloop<NT>(acc, sm, xl, wt, KT);
 
-    // h = silu(g) * u: channels hw + 16*t + 4*(L/16) + i, token 16*j + L%16
-    float hv[2][NT][4];
+    // h = silu(g) * u: channels hw + 4*(L/16) + i, token 16*j + L%16
+    float hv[NT][4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float g = acc[t][j][i], u = acc[t + 2][j][i];
-                hv[t][j][i] = (g / (1.0f + __expf(-g))) * u;
-            }
+        for (int i = 0; i < 4; ++i) {
+            const float g = acc[0][j][i], u = acc[1][j][i];
+            hv[j][i] = (g / (1.0f + __expf(-g))) * u;
+        }
     const int I128 = I >> 7;
-    float inv[NT];
     if (p.ffn_ue8m0) {
-        // amax over the block's 128 hidden columns = the 4 waves; the LDS
+        // amax over the block's 128 hidden columns = the 8 waves; the LDS
         // tiles are free after the main loop's last barrier.
-        float* red = reinterpret_cast<float*>(&sm.x[0][0]);   // [4][kBigRows]
+        float* red = reinterpret_cast<float*>(&sm.x[0][0]);   // [8][kBigRows]
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            float m = 0.f;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(hv[t][j][i]));
+            float m = fmaxf(fmaxf(fabsf(hv[j][0]), fabsf(hv[j][1])),
+                            fmaxf(fabsf(hv[j][2]), fabsf(hv[j][3])));
             m = fmaxf(m, __shfl_xor(m, 16, 64));
             m = fmaxf(m, __shfl_xor(m, 32, 64));
             if (lane < 16) red[wave * kBigRows + 16 * j + lane] = m;
@@ -377,26 +368,25 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
             const int r = 16 * j + (lane & 15);
             float amax = red[r];
 #pragma unroll
-            for (int w = 1; w < 4; ++w) amax = fmaxf(amax, red[w * kBigRows + r]);
+            for (int w = 1; w < kWaves; ++w) amax = fmaxf(amax, red[w * kBigRows + r]);
             const uint32_t sb = block_scale_byte(amax);
-            inv[j] = inv_scale(sb);
-            if (wave == 0 && lane < 16 && r < it.rows)
-                p.out_sf[(size_t)(it.off + it.m0 + r) * I128 + it.bx] = (uint8_t)sb;
+            const float inv = inv_scale(sb);
+            if (r < it.rows) {
+                const size_t slot = (size_t)(it.off + it.m0 + r);
+                *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 4 * (lane >> 4)) =
+                    pack4_fp8(hv[j][0] * inv, hv[j][1] * inv, hv[j][2] * inv, hv[j][3] * inv);
+                if (wave == 0 && lane < 16) p.out_sf[slot * I128 + it.bx] = (uint8_t)sb;
+            }
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) inv[j] = 1.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const int r = 16 * j + (lane & 15);
-        if (r < it.rows) {
-            uint8_t* dst = p.out8 + (size_t)(it.off + it.m0 + r) * I + hw + 4 * (lane >> 4);
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-                *reinterpret_cast<uint32_t*>(dst + 16 * t) =
-                    pack4_fp8(hv[t][j][0] * inv[j], hv[t][j][1] * inv[j], hv[t][j][2] * inv[j],
-                              hv[t][j][3] * inv[j]);
+        for (int j = 0; j < NT; ++j) {
+            const int r = 16 * j + (lane & 15);
+            if (r < it.rows) {
+                const size_t slot = (size_t)(it.off + it.m0 + r);
+                *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 4 * (lane >> 4)) =
+                    pack4_fp8(hv[j][0], hv[j][1], hv[j][2], hv[j][3]);
+            }
         }
     }
 }
@@ -409,7 +399,7 @@ __global__ void __launch_bounds__(kBigThreads) l1_big_kernel(GemmParams p) {
     if (!big_unit(p, p.I / kL1BlockH, it)) return;
     const int KT = p.H >> 7, I = p.I, G = p.G;
     const int tiles = (it.rows + 15) >> 4;
-    // scales: x rows through perm[]; W1 tiles 4*wave + {gate, gate, up, up}
+    // scales: x rows through perm[]; W1 tiles 2*wave (gate), 2*wave+1 (up)
     big_load_scales(
         sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
         [&](int r) {
@@ -417,8 +407,8 @@ __global__ void __launch_bounds__(kBigThreads) l1_big_kernel(GemmParams p) {
             return p.x_sf + (size_t)(p.perm[slot] / (uint32_t)p.topk) * KT;
         },
         [&](int t) {
-            const int hw = it.bx * kL1BlockH + (t >> 2) * 32;
-            const int rho = (hw / G) * 2 * G + (hw % G) + ((t & 2) ? G : 0);
+            const int hw = it.bx * kL1BlockH + (t >> 1) * 16;
+            const int rho = (hw / G) * 2 * G + (hw % G) + ((t & 1) ? G : 0);
             return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
         });
 #define MM_L1_BODY(n) l1_big_body<n>(p, it, sm)
@@ -436,7 +426,7 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     big_loader_init<NT>(xl, [&](int r) {
         return (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
     });
-    const int n0 = it.bx * kL2BlockN + wave * 64;   // this wave's 64 output channels
+    const int n0 = it.bx * kL2BlockN + wave * 32;   // this wave's 32 output channels
     const uint8_t* we = p.w + (size_t)it.e * (size_t)H * I;
     const size_t tstride = (size_t)KT * kTileBytes;
     const uint8_t* wt[kWT];

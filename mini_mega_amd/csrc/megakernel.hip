@@ -22,8 +22,8 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 int auto_m_tile(int tokens, int topk, int E) {
     // Rows per work item: one item per expert when the expected expert load
     // (plus the spread of a random router) fits, so that each expert's weights
-    // stream from HBM once.  <= 32 rows: decode-shaped kernels; 64..192: the
-    // LDS-staged kernels (up to 12 token tiles per item).
+    // stream from HBM once.  <= 32 rows: decode-shaped kernels; 64..256: the
+    // LDS-staged kernels (up to 16 token tiles per item).
     const double mean = (double)tokens * topk / (E > 0 ? E : 1);
     if (mean <= 20.0) return 32;
     if (mean <= 44.0) return 64;

@@ -13,8 +13,8 @@ constexpr int kRouteThreads = 256;
 constexpr int kRouteChunk = 1024;   // pairs per routing chunk
 
 constexpr int kGemmThreads = 256;   // 4 waves per workgroup (decode-shaped GEMMs)
-constexpr int kBigThreads = 256;    // 4 waves per workgroup, one per SIMD (large-M GEMMs)
-constexpr int kBigMaxTiles = 12;    // large-M GEMMs: up to 12 token tiles (192 rows) per item
+constexpr int kBigThreads = 512;    // 8 waves per workgroup, two per SIMD (large-M GEMMs)
+constexpr int kBigMaxTiles = 16;    // large-M GEMMs: up to 16 token tiles (256 rows) per item
 constexpr int kBigMaxKT = 64;       // large-M GEMMs: K / 128 <= 64 (H, I <= 8192)
 constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 workgroup
 constexpr int kL2BlockN = 256;      // output channels per L2 workgroup

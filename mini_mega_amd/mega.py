@@ -29,7 +29,7 @@ from . import _lib
 from ._lib import MegaLaunchArgs, check, lib
 
 _SUPPORTED_MMA_TYPES = ("fp8xfp8", "bf16xfp8")
-EXPERT_WINDOW_CHOICES = (0, 16, 32, 64, 128, 192)
+EXPERT_WINDOW_CHOICES = (0, 16, 32, 64, 128, 256)
 
 
 def _align(x: int, a: int) -> int:
