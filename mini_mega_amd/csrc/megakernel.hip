@@ -22,10 +22,11 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 int auto_m_tile(int tokens, int topk, int E) {
     // Rows per work item: one item per expert when the expected expert load
     // (plus the spread of a random router) fits, so that each expert's weights
-    // stream from HBM once.  <= 32 rows: decode-shaped kernels; 64..256: the
-    // LDS-staged kernels (up to 16 token tiles per item).
+    // stream from HBM once.  The LDS-staged 8-wave kernels (64..256 rows) are
+    // at least as fast as the decode-shaped ones (win_cap 16/32) from T = 512
+    // (measured on MI355X: L1 955 vs 1003 us, L2 568 vs 591 us), so the
+    // automatic choice always uses them.
     const double mean = (double)tokens * topk / (E > 0 ? E : 1);
-    if (mean <= 20.0) return 32;
     if (mean <= 44.0) return 64;
     if (mean <= 96.0) return 128;
     return 16 * mm::kBigMaxTiles;

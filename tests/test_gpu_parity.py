@@ -192,7 +192,8 @@ SMALL = [
     (32, 8, 1024, 512, 160, False, 64),
     (16, 4, 512, 256, 600, True, 128),
     (8, 8, 256, 128, 300, True, 128),    # every token routed to every expert: 3 items each
-    (24, 6, 1024, 512, 700, True, 0),    # auto tile: 175 rows per expert -> 2 items of <= 128
+    (8, 8, 256, 128, 250, True, 256),    # 250 rows per expert: one item of 16 token tiles
+    (24, 6, 1024, 512, 700, True, 0),    # auto tile: 175 rows per expert -> one 256-row window
 ]
 
 
