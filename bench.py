@@ -220,7 +220,7 @@ def main():
     b2 = l2_bytes(counts)
     a2 = b2 / (ms_l2 * 1e-3) / 1e9
 
-    traffic, traffic_src = profiled_traffic(T, "mm::l1_kernel")
+    traffic, traffic_src = profiled_traffic(T, "mm::l1_big_kernel")
     out = {
         "metric": "MoE layer µs + TFLOPS + HBM GB/s (% roofline), E256 top8 H6144 I2048, "
                   "T=512/2048/8192",
@@ -248,7 +248,7 @@ def main():
                        "l2": round(ms_l2 * 1e3, 1), "combine": round(ms_red * 1e3, 1)},
         "l2_kernel": {"achieved": round(a2, 1), "unit": "GB/s", "frac": round(a2 / HBM_PEAK_GBS, 4),
                       "bytes": b2},
-        "roofline": {"bound": "hbm", "kernel": "l1_kernel (grouped gate/up GEMM + SwiGLU)",
+        "roofline": {"bound": "hbm", "kernel": "l1_big_kernel (grouped gate/up GEMM + SwiGLU)",
                      "achieved": round(a1, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(a1 / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src, "algorithmic_bytes": b1},
