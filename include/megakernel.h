@@ -161,6 +161,14 @@ int last_error();
 // Logical row-major [n_mats][n_rows][k_cols] fp8 -> tile layout.
 void pack_weights(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows,
                   int k_cols, hipStream_t stream);
+// The reference's packed on-device weights (lane-tile layout: fill_w_lane
+// bytes, src/megakernel.cu:66-105, closed form src/bench_check.cuh:268-272;
+// the output of its transform_weights_for_mega_moe,
+// torch/mxmegakernel/mega/__init__.py:553-573) -> tile layout.  The logical
+// row order is kept (W1 rows stay gate/up paired).  n_rows % 32 == 0,
+// k_cols % 128 == 0.
+void pack_weights_from_reference(uint8_t* dst, const uint8_t* src, int n_mats,
+                                 int n_rows, int k_cols, hipStream_t stream);
 // Synthetic N(0, sigma) weights quantised with 128x128 UE8M0 block scales,
 // written in tile layout + scales [n_mats][n_rows/128][k_cols/128].
 void fill_weights_normal(uint8_t* w, uint8_t* w_sf, int n_mats, int n_rows,
@@ -203,6 +211,8 @@ int mm_fill_weights_lane(uint8_t* w, int n_rows, int k_cols, unsigned seed,
                          void* stream);
 int mm_pack_weights(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows,
                     int k_cols, void* stream);
+int mm_pack_weights_from_reference(uint8_t* dst, const uint8_t* src, int n_mats,
+                                   int n_rows, int k_cols, void* stream);
 int mm_fill_weights_normal(uint8_t* w, uint8_t* w_sf, int n_mats, int n_rows,
                            int k_cols, unsigned long long seed, float sigma,
                            void* stream);

@@ -12,10 +12,13 @@ from .mega import (  # noqa: F401
     fp8_mega_moe,
     fp8_mega_moe_compute,
     fp8_mega_moe_reduce,
+    fold_checkpoint_block_scales,
     get_symm_buffer_for_mega_moe,
     get_symm_buffer_size_for_mega_moe,
     get_token_alignment_for_mega_moe,
     pack_weights,
+    pack_weights_from_reference,
     pairing_block,
     transform_weights_for_mega_moe,
+    transform_weights_from_reference,
 )

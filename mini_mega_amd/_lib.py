@@ -62,6 +62,7 @@ EXPORTS = (
     "mm_abi_version", "mm_args_size", "mm_args_offset", "mm_layout", "mm_launch_prelude",
     "mm_launch_compute", "mm_launch_l1", "mm_launch_l2", "mm_launch_reduce", "mm_launch_full",
     "mm_launch_empty", "mm_launch_dispatch", "mm_fill_weights_lane", "mm_pack_weights",
+    "mm_pack_weights_from_reference",
     "mm_fill_weights_normal", "mm_quant_act", "mm_selftest_convert", "mm_dump_kernel_resources",
 )
 
@@ -97,6 +98,8 @@ def lib():
     L.mm_fill_weights_lane.argtypes = [c_vp, c_int, c_int, ctypes.c_uint, c_vp]
     L.mm_pack_weights.restype = c_int
     L.mm_pack_weights.argtypes = [c_vp, c_vp, c_int, c_int, c_int, c_vp]
+    L.mm_pack_weights_from_reference.restype = c_int
+    L.mm_pack_weights_from_reference.argtypes = [c_vp, c_vp, c_int, c_int, c_int, c_vp]
     L.mm_fill_weights_normal.restype = c_int
     L.mm_fill_weights_normal.argtypes = [c_vp, c_vp, c_int, c_int, c_int, ctypes.c_ulonglong,
                                          c_float, c_vp]

@@ -1,5 +1,6 @@
 // aux.hip -- data-preparation kernels: deterministic and synthetic weight
-// generators in the tile layout, logical -> tile packing, bf16 -> fp8
+// generators in the tile layout, logical -> tile packing, the reference's
+// lane-tile layout -> tile layout, bf16 -> fp8
 // activation cast, a conversion self-test, the empty kernel and a fill.
 #include "mm_kernels.h"
 
@@ -54,6 +55,38 @@ pack_weights_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, 
         slot_coords(j, KT, row, k);
         const uint8_t* s = src + (m * n_rows + row) * (size_t)k_cols + k;
         *reinterpret_cast<v4i*>(dst + i * 16) = *reinterpret_cast<const v4i*>(s);
+    }
+}
+
+// The reference's on-device lane-tile layout -> this library's tile layout,
+// 16 bytes per thread.  Reference byte (row, k) of a [n_rows][k_cols] matrix
+// sits at ((row/32)*(k_cols/32) + k/32)*1024 + L*16 + ((row/16)&1)*8 + k%8 with
+// L = row%16 + ((k%32)/8)*16 (closed form src/bench_check.cuh:268-272; the
+// torch-side _swizzle_lane, torch/mxmegakernel/mega/__init__.py:512-533), so
+// the 16 logical bytes of a destination slot are two 8-byte pieces.
+__global__ void __launch_bounds__(256)
+pack_weights_ref_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, int n_mats,
+                        int n_rows, int k_cols) {
+    const int KT = k_cols >> 7;
+    const size_t per_mat = (size_t)(n_rows >> 4) * KT * 128;
+    const size_t total = per_mat * n_mats;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t m = i / per_mat, j = i % per_mat;
+        int row, k;
+        slot_coords(j, KT, row, k);
+        const uint8_t* base = src + m * (size_t)n_rows * k_cols;
+        uint2 piece[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int kk = k + 8 * h;
+            const int L = (row & 15) + ((kk & 31) >> 3) * 16;
+            const size_t off = ((size_t)(row >> 5) * (k_cols >> 5) + (kk >> 5)) * 1024 +
+                               L * 16 + ((row >> 4) & 1) * 8;
+            piece[h] = *reinterpret_cast<const uint2*>(base + off);
+        }
+        *reinterpret_cast<v4i*>(dst + i * 16) =
+            v4i{(int)piece[0].x, (int)piece[0].y, (int)piece[1].x, (int)piece[1].y};
     }
 }
 

@@ -304,6 +304,19 @@ void pack_weights(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows, int 
     record(launched(kOk));
 }
 
+void pack_weights_from_reference(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows,
+                                 int k_cols, hipStream_t s) {
+    if (!dst || !src) { record(kErrNullPointer); return; }
+    if (n_mats <= 0 || n_rows <= 0 || n_rows % 32 || k_cols <= 0 || k_cols % 128) {
+        record(kErrBadDims);
+        return;
+    }
+    const size_t slots = (size_t)n_mats * (n_rows / 16) * (k_cols / 128) * 128;
+    hipLaunchKernelGGL(mm::pack_weights_ref_kernel, dim3(grid_for(slots)), dim3(256), 0, s, dst,
+                       src, n_mats, n_rows, k_cols);
+    record(launched(kOk));
+}
+
 void fill_weights_normal(uint8_t* w, uint8_t* w_sf, int n_mats, int n_rows, int k_cols,
                          uint64_t seed, float sigma, hipStream_t s) {
     if (!w || !w_sf) { record(kErrNullPointer); return; }
@@ -419,6 +432,12 @@ int mm_fill_weights_lane(uint8_t* w, int n_rows, int k_cols, unsigned seed, void
 int mm_pack_weights(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows, int k_cols,
                     void* stream) {
     fp8mega::pack_weights(dst, src, n_mats, n_rows, k_cols, (hipStream_t)stream);
+    return fp8mega::last_error();
+}
+
+int mm_pack_weights_from_reference(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows,
+                                   int k_cols, void* stream) {
+    fp8mega::pack_weights_from_reference(dst, src, n_mats, n_rows, k_cols, (hipStream_t)stream);
     return fp8mega::last_error();
 }
 

@@ -53,6 +53,7 @@ __global__ void combine_kernel(const uint16_t*, const int*, const float*, int, i
                                uint16_t*);
 __global__ void fill_w_lane_kernel(uint8_t*, int, int, uint32_t);
 __global__ void pack_weights_kernel(uint8_t*, const uint8_t*, int, int, int);
+__global__ void pack_weights_ref_kernel(uint8_t*, const uint8_t*, int, int, int);
 __global__ void fill_weights_normal_kernel(uint8_t*, uint8_t*, int, int, uint64_t, float);
 __global__ void quant_act_kernel(const uint16_t*, int, int, uint8_t*, uint8_t*);
 __global__ void convert_selftest_kernel(const float*, int, uint8_t*, uint16_t*);

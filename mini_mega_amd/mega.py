@@ -21,6 +21,7 @@ Every call enqueues HIP kernels on torch's current stream through the C ABI
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Optional, Tuple, Union
 
 import torch
@@ -286,6 +287,80 @@ def transform_weights_for_mega_moe(
         return l1_t, l2_t
     s1p = _interleave_rows(_sf_to_ue8m0(s1), G // 128)
     return (l1_t, s1p), (l2_t, _sf_to_ue8m0(s2).contiguous())
+
+
+def pack_weights_from_reference(w: torch.Tensor) -> torch.Tensor:
+    """The reference's packed [E, N, K] fp8 (lane-tile layout of its
+    _swizzle_lane, torch/mxmegakernel/mega/__init__.py:512-533) -> this
+    library's tile layout, keeping the logical row order (device kernel)."""
+    if w.dim() == 2:
+        w = w.unsqueeze(0)
+    e, n, k = w.shape
+    src = w.contiguous().view(torch.uint8)
+    dst = torch.empty_like(src)
+    check("mm_pack_weights_from_reference",
+          lib().mm_pack_weights_from_reference(dst.data_ptr(), src.data_ptr(), e, n, k,
+                                               _stream_ptr()))
+    return dst.view(torch.float8_e4m3fn)
+
+
+def transform_weights_from_reference(
+        l1_weights: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
+        l2_weights: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]):
+    """Weights already packed for the reference (the output of its
+    transform_weights_for_mega_moe, torch/mxmegakernel/mega/__init__.py:553-573:
+    W1 gate/up paired every 256 rows, then lane-swizzled; W2 lane-swizzled)
+    -> this library's packed weights, as transform_weights_for_mega_moe
+    returns them.  The reference pairs W1 in blocks of 256, which equals
+    this library's block min(256, I) since the reference needs I % 256 == 0.
+    Optional UE8M0 scales, given as (w, sf) tuples, are in the torch layout
+    ([E, 2I/128, H/128] with [gate | up] rows, [E, H/128, I/128])."""
+    w1, s1 = _split(l1_weights)
+    w2, s2 = _split(l2_weights)
+    for name, t in (("l1_weights", w1), ("l2_weights", w2)):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.float8_e4m3fn:
+            raise TypeError(f"{name} must be a float8_e4m3fn tensor")
+    I = w1.shape[-2] // 2
+    if I % 256 != 0:
+        raise ValueError(f"reference-packed W1 needs I % 256 == 0 (its pairing block); got I={I}")
+    if (s1 is None) != (s2 is None):
+        raise ValueError("give scales for both l1 and l2 or for neither")
+    squeeze = w1.dim() == 2
+    l1_t = pack_weights_from_reference(w1)
+    l2_t = pack_weights_from_reference(w2)
+    if squeeze:
+        l1_t, l2_t = l1_t.squeeze(0), l2_t.squeeze(0)
+    if s1 is None:
+        return l1_t, l2_t
+    s1 = s1.unsqueeze(0) if s1.dim() == 2 else s1
+    s1p = _interleave_rows(_sf_to_ue8m0(s1), pairing_block(I) // 128)
+    s2p = _sf_to_ue8m0(s2).contiguous()
+    if squeeze:
+        s1p = s1p.squeeze(0)
+    return (l1_t, s1p), (l2_t, s2p)
+
+
+def fold_checkpoint_block_scales(w13: torch.Tensor, w13_sf: torch.Tensor, w2: torch.Tensor,
+                                 w2_sf: torch.Tensor):
+    """The reference serving path's raw-E4M3 weight build from a block-scaled
+    fp8 checkpoint (torch/sglang_patches/patch_mega_scale.py:19-30): dequantise
+    with the 128x128 block scales, cast W1 directly (clamped to +-448; SwiGLU
+    does not allow folding a scale back out), and scale W2 by the power of two
+    w2_scale = 2^floor(log2(448 / amax(W2))) before its cast.  The caller
+    divides the top-k weights by w2_scale so that REDUCE cancels it exactly.
+    Returns (w13_raw, w2_raw, w2_scale).  (This library can instead keep the
+    block scales: pass (w, sf) tuples to transform_weights_for_mega_moe.)"""
+    def dequant(w, sf):
+        e, n, k = w.shape
+        f = sf.to(torch.float32).repeat_interleave(128, dim=1).repeat_interleave(128, dim=2)
+        return w.to(torch.float32) * f[:, :n, :k]
+    w13_f = dequant(w13, w13_sf)
+    w2_f = dequant(w2, w2_sf)
+    amax2 = float(w2_f.abs().max())
+    w2_scale = 2.0 ** math.floor(math.log2(448.0 / amax2)) if amax2 > 0 else 1.0
+    w13_raw = w13_f.clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    w2_raw = (w2_f * w2_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return w13_raw, w2_raw, w2_scale
 
 
 # ------------------------------------------------------------------ launches

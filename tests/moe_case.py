@@ -306,3 +306,19 @@ def check_e2e_tokens(c: Case, r: Run, tokens, nthreads: int = 16):
     assert err <= E2E_ABS_FRAC * rms and cos >= E2E_COS, (
         f"end-to-end (token subset): max_abs {err:.3e} rms {rms:.3e} cos {cos:.6f}")
     return err, rms, cos
+
+def ref_lane_pack(w):
+    """Logical [E][N][K] uint8 -> the reference's on-device lane-tile bytes:
+    byte (row, k) at ((row/32)*(K/32) + k/32)*1024 + L*16 + ((row/16)&1)*8 +
+    k%8 with L = row%16 + ((k%32)/8)*16 (src/bench_check.cuh:268-272)."""
+    e, n, k = w.shape
+    row = np.arange(n)[:, None]
+    kk = np.arange(k)[None, :]
+    lane = (row % 16) + ((kk % 32) // 8) * 16
+    off = ((row // 32) * (k // 32) + kk // 32) * 1024 + lane * 16 + ((row // 16) & 1) * 8 + kk % 8
+    out = np.empty_like(w)
+    for m in range(e):
+        flat = np.empty(n * k, dtype=w.dtype)
+        flat[off.ravel()] = w[m].ravel()
+        out[m] = flat.reshape(n, k)
+    return out

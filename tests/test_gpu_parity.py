@@ -69,6 +69,40 @@ def test_pack_weights_roundtrip():
         assert np.array_equal(inputs.unpack_tiles(p[e].ravel(), 64, 384), w[e])
 
 
+@pytest.mark.parametrize("scaled", [False, True])
+def test_transform_from_reference_layout(scaled):
+    """Weights packed the reference's way (W1 gate/up paired every 256 rows,
+    then its lane tiles, src/bench_check.cuh:268-272) convert to exactly the
+    bytes transform_weights_for_mega_moe makes from the torch layout."""
+    _say(f"transform from reference layout scaled={scaled}")
+    E, H, I = 2, 384, 512
+    rng = np.random.default_rng(11)
+    w1 = rng.integers(0, 256, size=(E, 2 * I, H)).astype(np.uint8)
+    w2 = rng.integers(0, 256, size=(E, H, I)).astype(np.uint8)
+    # the reference's _interleave_weights(gran=256): [gate 0..255, up 0..255, gate 256..]
+    g = w1[:, :I].reshape(E, I // 256, 256, H)
+    u = w1[:, I:].reshape(E, I // 256, 256, H)
+    w1_paired = np.stack([g, u], axis=2).reshape(E, 2 * I, H)
+    r1 = torch.from_numpy(mc.ref_lane_pack(w1_paired)).cuda().view(torch.float8_e4m3fn)
+    r2 = torch.from_numpy(mc.ref_lane_pack(w2)).cuda().view(torch.float8_e4m3fn)
+    t1 = torch.from_numpy(w1).cuda().view(torch.float8_e4m3fn)
+    t2 = torch.from_numpy(w2).cuda().view(torch.float8_e4m3fn)
+    if scaled:
+        s1 = torch.from_numpy(rng.integers(120, 135, size=(E, 2 * I // 128, H // 128))
+                              .astype(np.uint8)).cuda()
+        s2 = torch.from_numpy(rng.integers(120, 135, size=(E, H // 128, I // 128))
+                              .astype(np.uint8)).cuda()
+        (a1, as1), (a2, as2) = mm.transform_weights_from_reference((r1, s1), (r2, s2))
+        (b1, bs1), (b2, bs2) = mm.transform_weights_for_mega_moe((t1, s1), (t2, s2))
+        assert torch.equal(as1, bs1) and torch.equal(as2, bs2)
+    else:
+        a1, a2 = mm.transform_weights_from_reference(r1, r2)
+        b1, b2 = mm.transform_weights_for_mega_moe(t1, t2)
+    torch.cuda.synchronize()
+    assert torch.equal(a1.view(torch.uint8), b1.view(torch.uint8))
+    assert torch.equal(a2.view(torch.uint8), b2.view(torch.uint8))
+
+
 def test_fill_weights_lane_matches_wprobe():
     _say("fill_weights_lane")
     n, k = 512, 768
