@@ -109,7 +109,7 @@ struct MegaLayout {
     int64_t chunk_hist;    // int32[nchunks][E] per-chunk histograms -> prefixes
     int64_t counts;        // int32[E]   per-expert routed rows (after cap)
     int64_t offsets;       // int32[E+1] exclusive prefix of counts
-    int64_t items;         // int32[max_items][4] (expert, first row, end row, 0) work items
+    int64_t items;         // int32[max_items][4] (expert, first row, end row, j | n << 16) work items
     int64_t perm;          // uint32[P]  pair index per slot (canonical order)
     int64_t pair_pos;      // int32[P]   slot per pair or -1
     int64_t xq;            // uint8[max_tokens][H]     folded fp8 x (in_bf16)

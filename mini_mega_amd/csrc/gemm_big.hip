@@ -247,10 +247,16 @@ struct BigItem {
     int e, m0, rows, off, bx;
 };
 
-// Work unit u = item * nb + bx.  The XCDs take workgroups round-robin, so
-// workgroup L (the k-th of XCD L%8, k = L/8) runs unit (L%8)*c + k with
-// c = ceil(units / 8): each XCD walks a contiguous range.  The grid has
-// nb * max_items + 8 workgroups, enough for 8*c; the surplus exits.
+// Work units: an expert with n items has n * nb units, numbered from
+// nb * (its first item) on, block-major: unit nb*i0 + bx*n + j is block bx of
+// item i0 + j.  The n items of an expert read the same weight blocks, and
+// this order runs the n readers of each block on neighbouring CUs of one XCD
+// at the same time, so all but one take the block from that XCD's L2.  (The
+// expert of unit u is the one of item u / nb: its items are consecutive.)
+// The XCDs take workgroups round-robin, so workgroup L (the k-th of XCD L%8,
+// k = L/8) runs unit (L%8)*c + k with c = ceil(units / 8): each XCD walks a
+// contiguous range.  The grid has nb * max_items + 8 workgroups, enough for
+// 8*c; the surplus exits.
 __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& it) {
     const int units = nb * p.status[1];
     const int c = (units + 7) >> 3;
@@ -258,9 +264,13 @@ __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& i
     const int k = L >> 3;
     const int u = (L & 7) * c + k;
     if (k >= c || u >= units) return false;
-    const int item = u / nb;
-    it.bx = u - item * nb;
-    const int4 v = reinterpret_cast<const int4*>(p.items)[item];
+    const int4* items = reinterpret_cast<const int4*>(p.items);
+    const int im = u / nb;                 // item-major item: same expert
+    const int jn = items[im].w;
+    const int i0 = im - (jn & 0xffff), n = jn >> 16;
+    const int local = u - nb * i0;
+    it.bx = local / n;
+    const int4 v = items[i0 + local % n];
     it.e = v.x;
     it.m0 = v.y;
     it.rows = v.z - v.y;

@@ -28,7 +28,8 @@ struct GemmParams {
     const uint8_t* w_sf;      // UE8M0 block scales [E][N/128][K/128] or null
     const int* counts;        // [E]
     const int* offsets;       // [E+1]
-    const int* items;         // [max_items][4]: expert, first row, end row, 0
+    const int* items;         // [max_items][4]: expert, first row, end row, j | n << 16
+                              // (item j of the expert's n)
     const int* status;        // [1] = number of items
     const uint32_t* perm;     // slot -> pair (L1 gathers x rows through it)
     uint8_t* out8;            // L1: ffn fp8 [P][I]

@@ -87,7 +87,8 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
     if (threadIdx.x == 0) offsets[E] = slots;
     // Work items: the expert's rows split evenly into ceil(cnt / m_tile)
     // items of at most m_tile rows (no item re-streams the expert's weights
-    // for a small remainder).
+    // for a small remainder).  Record: (expert, first row, end row,
+    // index within the expert | item count of the expert << 16).
     const int nm = (cnt + m_tile - 1) / m_tile;
     const int sz = nm > 0 ? (cnt + nm - 1) / nm : 0;
     int nitems = 0;
@@ -96,7 +97,7 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
         const int it = ioff + j;
         if (it < max_items) {
             const int m0 = j * sz;
-            reinterpret_cast<int4*>(items)[it] = make_int4(e, m0, min(cnt, m0 + sz), 0);
+            reinterpret_cast<int4*>(items)[it] = make_int4(e, m0, min(cnt, m0 + sz), j | (nm << 16));
         }
     }
     if (threadIdx.x == 0) {

@@ -159,6 +159,11 @@ class SymmBuffer:
     def status(self):
         return self._ws(self.layout.status, torch.int32, (16,))
 
+    def items(self, n: int):
+        """Work items: (expert, first row, end row, j | n << 16 for item j of
+        the expert's n)."""
+        return self._ws(self.layout.items, torch.int32, (n, 4))
+
     def make_args(self, num_tokens: int, l1, l2, y_bf16: Optional[torch.Tensor] = None,
                   y_fp32: Optional[torch.Tensor] = None, skip_prologue: int = 0,
                   slot_capacity: int = 0) -> MegaLaunchArgs:

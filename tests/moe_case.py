@@ -121,6 +121,18 @@ def check_routing(c: Case, r: Run):
     assert np.array_equal(r.perm, perm), "canonical permutation differs"
     assert np.array_equal(r.pair_pos, pair_pos), "pair slots differ"
     assert r.status[0] == 0, f"device status word {r.status[0]}"
+    # work items: each expert's rows split evenly into ceil(count / m_tile) items
+    m_tile = int(r.buf.layout.m_tile)
+    want = []
+    for e, cnt in enumerate(counts.tolist()):
+        if cnt == 0:
+            continue
+        nm = -(-cnt // m_tile)
+        sz = -(-cnt // nm)
+        want += [(e, j * sz, min(cnt, (j + 1) * sz), j | (nm << 16)) for j in range(nm)]
+    assert int(r.status[1]) == len(want), "work item count differs"
+    got = r.buf.items(len(want)).cpu().numpy() if want else np.zeros((0, 4), np.int32)
+    assert np.array_equal(got, np.array(want, dtype=np.int32).reshape(-1, 4)), "work items differ"
 
 
 def _bad(got, want, rel, abs_tol):
