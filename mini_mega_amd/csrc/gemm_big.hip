@@ -7,24 +7,27 @@
 // 1375-1679), the reference's count-tiered big-window GEMMs.
 //
 // One 8-wave workgroup (two waves per SIMD) per work unit = (work item,
-// block of 256 weight rows); each wave owns a 32-row weight slice (two
-// 16-row tiles) across all of the item's token rows (up to 256, so that at
+// block of 256 weight rows = 16 tiles); each wave owns a 32-row weight slice
+// (two 16-row tiles).  The code is written for W waves of 16/W tiles each;
+// W = 4 (one wave per SIMD, four tiles, accumulators in AGPRs: half the LDS
+// operand traffic per MFMA) was measured slower at every T on MI355X (T =
+// 8192 with items of <= 192 rows: L1 3423 vs 3254 us), so only W = 8 is
+// instantiated.  Each wave covers all of the item's token rows (up to 256, so that at
 // T = 8192 one item covers an expert and its weights stream from HBM once):
-//   * per 128-k step, the 512 threads gather the item's active token rows
-//     (through perm[] for L1, slot order for L2), convert them once to bf16
-//     with the row's UE8M0 scale folded in (exact), and store them in a
+//   * per 128-k step, the workgroup gathers the item's active token rows
+//     (through perm[] for L1, slot order for L2), converts them once to bf16
+//     with the row's UE8M0 scale folded in (exact), and stores them in a
 //     double-buffered LDS tile: [token tile][k-group q][lane][8 bf16], so that
-//     a wave's operand read for one MFMA pair is 1 KiB contiguous (the LDS
-//     reads then run at ~2/3 of the measured ~190 B/clk/CU at full MFMA rate);
-//   * each wave streams its two weight tiles (L1: gate and up rows of 16
-//     hidden columns; L2: 32 output channels) from HBM through a 3- or
-//     4-stage register pipeline and converts them exactly to bf16;
+//     a wave's operand read for one MFMA group is 1 KiB contiguous;
+//   * each wave streams its weight tiles (L1: gate and up rows of its hidden
+//     columns; L2: its output channels) from HBM through a 2- to 6-stage
+//     register pipeline and converts them exactly to bf16;
 //   * v_mfma_f32_16x16x32_bf16 (fp32-accurate sums; see gemm.hip) over the
 //     item's NT active token tiles -- NT is a compile-time specialisation
 //     picked per item (1..8, then even up to 16), so the k loop has no branch
-//     and the 2*NT accumulators (up to 128 registers) are independent chains;
+//     and the accumulator chains are independent;
 //   * epilogues as in gemm.hip: L1 SwiGLU + fp8 (raw, or per-128 UE8M0 with
-//     the 128-column amax reduced over the 8 waves in LDS), L2 bf16.
+//     the 128-column amax reduced over the waves in LDS), L2 bf16.
 // Work units are numbered so that each XCD runs a contiguous range of them:
 // the N-blocks of one item share that XCD's L2 for the item's activations.
 #include "mm_kernels.h"
@@ -32,10 +35,17 @@
 namespace mm {
 
 constexpr int kXTileBytes = 16 * kTileK * 2;   // one bf16 token tile: 16 rows x 128 k
-constexpr int kWaves = kBigThreads / 64;        // 8
-constexpr int kWT = 2;                          // weight tiles per wave
-constexpr int kBlockTiles = kWaves * kWT;       // 16 weight tiles = 256 rows per workgroup
+constexpr int kBlockTiles = 16;                 // weight tiles = 256 rows per workgroup
 constexpr int kBigRows = kBigMaxTiles * 16;     // token rows per work item (max)
+static_assert(kBlockTiles * 16 == kL2BlockN && kBlockTiles * 8 == kL1BlockH, "block shape");
+
+// Workgroup shape: W waves, kWT = 16 / W weight tiles per wave.
+template <int W>
+struct Geo {
+    static constexpr int kWaves = W;
+    static constexpr int kThreads = 64 * W;
+    static constexpr int kWT = kBlockTiles / W;
+};
 
 struct alignas(16) BigSmem {
     uint8_t x[2][kBigMaxTiles * kXTileBytes];   // bf16 tiles, double buffered
@@ -43,26 +53,28 @@ struct alignas(16) BigSmem {
     uint8_t sfw[kBigMaxKT][kBlockTiles];        // the block's weight-tile scales [k-step][tile]
 };
 
-// Loader for NT active token tiles: chunk i = (tid + 512*u) mod (NT*128) is
-// row r = 16*(i/128) + i%16 of the item, fp8 bytes [16*cc, 16*cc+16) of the
-// k-step with cc = (i/16)%8: k-group g = cc/2, MFMA groups q = 2*(cc%2) and
-// q+1.  Rows vary fastest, so the 16 lanes of an LDS write phase fill 16
-// consecutive 16-byte slots (no bank conflicts).  When NT*128 is not a
-// multiple of 512 some threads redo another thread's chunk (same bytes to
-// the same LDS slot), which keeps every thread's work uniform.  XS register
-// stages: with two (NT <= 12), the rows of k-step kt+2 are in flight while
-// kt+1 is written to LDS; with one (larger NT: registers go to accumulators,
-// and a k-step's MFMAs alone cover an L2 hit), kt+1 is loaded during kt.
-template <int NT>
+// Loader for NT active token tiles: chunk i = (tid + T*u) mod (NT*128), T
+// the workgroup's threads, is row r = 16*(i/128) + i%16 of the item, fp8
+// bytes [16*cc, 16*cc+16) of the k-step with cc = (i/16)%8: k-group g = cc/2,
+// MFMA groups q = 2*(cc%2) and q+1.  Rows vary fastest, so the 16 lanes of an
+// LDS write phase fill 16 consecutive 16-byte slots (no bank conflicts).
+// When NT*128 is not a multiple of T some threads redo another thread's
+// chunk (same bytes to the same LDS slot), which keeps every thread's work
+// uniform.  XS register stages: with two, the rows of k-step kt+2 are in
+// flight while kt+1 is written to LDS; with one (where registers go to
+// accumulators, and a k-step's MFMAs alone cover an L2 hit), kt+1 is loaded
+// during kt.
+template <int W, int NT>
 struct XLoader {
-    static constexpr int U = (NT * 128 + kBigThreads - 1) / kBigThreads;
-    static constexpr int XS = NT > 12 ? 1 : 2;
+    static constexpr int kThreads = Geo<W>::kThreads;
+    static constexpr int U = (NT * 128 + kThreads - 1) / kThreads;
+    static constexpr int XS = (W == 8 || NT <= 8) ? 2 : 1;
     const uint8_t* base;
     uint32_t off[U];
     v4i reg[XS][U];
 
     __device__ __forceinline__ static int chunk(int u) {
-        return (threadIdx.x + kBigThreads * u) % (NT * 128);
+        return (threadIdx.x + kThreads * u) % (NT * 128);
     }
     __device__ __forceinline__ static int row_of(int i) { return ((i >> 7) << 4) | (i & 15); }
     __device__ __forceinline__ static int cc_of(int i) { return (i >> 4) & 7; }
@@ -89,50 +101,63 @@ struct XLoader {
     }
 };
 
+template <int WT>
 struct WStage {
-    v4i a[kWT][2];   // two weight tiles, two 16-byte halves each
+    v4i a[WT][2];   // the wave's weight tiles, two 16-byte halves each
 };
 
-__device__ __forceinline__ void w_load(WStage& w, const uint8_t* const* wt, int kt) {
+template <int WT>
+__device__ __forceinline__ void w_load(WStage<WT>& w, const uint8_t* const* wt, int kt) {
     const size_t o = (size_t)kt * kTileBytes;
 #pragma unroll
-    for (int t = 0; t < kWT; ++t) {
+    for (int t = 0; t < WT; ++t) {
         w.a[t][0] = load16_stream(wt[t] + o);
         w.a[t][1] = load16_stream(wt[t] + o + 1024);
     }
 }
 
 // Weight tile t's operand of k-group q (8 bf16 per lane) with scale s folded in.
-__device__ __forceinline__ v8bf w_group(const WStage& w, int t, int q, float s) {
+template <int WT>
+__device__ __forceinline__ v8bf w_group(const WStage<WT>& w, int t, int q, float s) {
     return fp8x8_to_bf16(w.a[t][q >> 1][2 * (q & 1)], w.a[t][q >> 1][2 * (q & 1) + 1], s);
 }
 
-// The wave's two weight-tile scale bytes of k-step kt (byte t = tile t).
+// The wave's weight-tile scale bytes of k-step kt (byte t = tile t).
+template <int WT>
 __device__ __forceinline__ uint32_t w_scales(const BigSmem& sm, int kt) {
     const int wave = threadIdx.x >> 6;
-    return *reinterpret_cast<const uint16_t*>(&sm.sfw[kt][kWT * wave]);
+    if constexpr (WT == 2)
+        return *reinterpret_cast<const uint16_t*>(&sm.sfw[kt][WT * wave]);
+    else
+        return *reinterpret_cast<const uint32_t*>(&sm.sfw[kt][WT * wave]);
 }
 
 __device__ __forceinline__ float scale_of(uint32_t bytes, int t) {
     return ue8m0_to_f32((bytes >> (8 * t)) & 0xffu);
 }
 
-// Weight register stages: 4 for NT <= 12 (even, so that two activation
-// stages alternate within a group), 3 above (registers; a k-step of >= 112
-// MFMA pairs per wave covers the latency of two steps ahead).
-template <int NT>
-constexpr int big_stages() { return NT > 12 ? 3 : 4; }
+// Weight register stages (even where the activations have two register
+// stages, so that these alternate within a group of S k-steps).  Up to 8
+// token tiles (8 waves): 4 for L1, 6 for L2, whose shorter units (K = I)
+// gain from the deeper prefetch (measured on MI355X at T = 512: L2 543 vs
+// 565 us; L1 prefers 4: 950 vs 961 us).  Above 12 tiles: 2, since the
+// registers go to accumulators and one k-step of >= 4*NT MFMA groups covers
+// the latency of the next step's weights.
+template <int W, int NT, bool L2>
+constexpr int big_stages() {
+    return (W == 8 ? NT > 12 : NT > 8) ? 2 : (W == 8 && NT <= 8 && L2 ? 6 : 4);
+}
 
-// Activation operand reads in flight ahead of their MFMAs: 3, or 2 above
-// NT = 12 (registers).
-template <int NT>
-constexpr int big_read_ahead() { return NT > 12 ? 2 : 3; }
+// Activation operand reads in flight ahead of their MFMAs: 3, or 2 for W = 8
+// above NT = 12 (registers).
+template <int W, int NT>
+constexpr int big_read_ahead() { return (W == 8 && NT > 12) ? 2 : 3; }
 
 // One k-step, software-pipelined by hand.  The step's 4*NT chunks (k-group
 // q, token tile j) each hold: the LDS read of the activation operand D
 // chunks ahead, a share of the conversions of the next k-group's weight
 // operands (in the last group: the next k-step's first), a share of the
-// activation commit of k-step kt+1 (last group only), and the chunk's 2
+// activation commit of k-step kt+1 (last group only), and the chunk's kWT
 // MFMAs.  A scheduling fence closes every chunk, so the compiler keeps this
 // order: operand reads stay ahead of their use, and conversions overlap the
 // MFMAs instead of stalling them.  Before the chunks: the prefetches of
@@ -141,24 +166,35 @@ constexpr int big_read_ahead() { return NT > 12 ? 2 : 3; }
 // compiler's wait counts stay partial).  After: the barrier that publishes
 // the committed activations.  a0 carries the converted k-group-0 operand from
 // one step to the next.
-template <int NT, int S, int s>
-__device__ __forceinline__ void big_step(v4f (&acc)[kWT][NT], BigSmem& sm, XLoader<NT>& xl,
-                                         WStage (&w)[S], const uint8_t* const* wt,
-                                         v8bf (&a0)[kWT], int kt, int KT) {
-    constexpr int XS = XLoader<NT>::XS, U = XLoader<NT>::U;
-    constexpr int G = 4 * NT, D = big_read_ahead<NT>() < G ? big_read_ahead<NT>() : G;
+template <int W, int NT, int S, int s>
+__device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
+                                         XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
+                                         const uint8_t* const* wt, v8bf (&a0)[Geo<W>::kWT],
+                                         int kt, int KT) {
+    constexpr int kWT = Geo<W>::kWT;
+    constexpr int XS = XLoader<W, NT>::XS, U = XLoader<W, NT>::U;
+    constexpr int G = 4 * NT, D = big_read_ahead<W, NT>() < G ? big_read_ahead<W, NT>() : G;
     constexpr int rs = XS == 2 ? ((s + 1) & 1) : 0;   // register stage holding k-step kt+1
     const int lane = threadIdx.x & 63;
     xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
-    w_load(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));
+    w_load<kWT>(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));
     // scale bytes, read here and decoded where used (no wait before the MFMAs)
     const int kn = min(kt + 1, KT - 1);
-    const uint32_t sc = w_scales(sm, kt), sn = w_scales(sm, kn);
+    const uint32_t sc = w_scales<kWT>(sm, kt), sn = w_scales<kWT>(sm, kn);
     uint32_t xs[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) xs[u] = sm.sfx[kn][XLoader<NT>::row_of(XLoader<NT>::chunk(u))];
-    const uint8_t* xb = &sm.x[kt & 1][lane * 16];
-    uint8_t* xw = &sm.x[(kt + 1) & 1][0];
+    for (int u = 0; u < U; ++u)
+        xs[u] = sm.sfx[kn][XLoader<W, NT>::row_of(XLoader<W, NT>::chunk(u))];
+    // LDS bases of this step's read and write buffers.  Opaque to the
+    // optimiser: otherwise it hoists every operand address of the unrolled
+    // group out of the loop into a register of its own (the buffer parity of
+    // each step is known there) instead of using one base plus immediate
+    // offsets.
+    uint32_t xro = (kt & 1) * (uint32_t)sizeof(sm.x[0]) + lane * 16;
+    uint32_t xwo = ((kt + 1) & 1) * (uint32_t)sizeof(sm.x[0]);
+    asm volatile("" : "+v"(xro), "+v"(xwo));
+    const uint8_t* xb = &sm.x[0][0] + xro;
+    uint8_t* xw = &sm.x[0][0] + xwo;
     v8bf b[D + 1];
 #pragma unroll
     for (int d = 0; d < D; ++d)
@@ -178,8 +214,8 @@ __device__ __forceinline__ void big_step(v4f (&acc)[kWT][NT], BigSmem& sm, XLoad
 #pragma unroll
         for (int t = 0; t < kWT; ++t)
             if (j == (t * NT) / kWT)
-                an[t] = q < 3 ? w_group(w[s], t, q + 1, scale_of(sc, t))
-                              : w_group(w[(s + 1) % S], t, 0, scale_of(sn, t));
+                an[t] = q < 3 ? w_group<kWT>(w[s], t, q + 1, scale_of(sc, t))
+                              : w_group<kWT>(w[(s + 1) % S], t, 0, scale_of(sn, t));
         if (q == 3) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
@@ -198,25 +234,40 @@ __device__ __forceinline__ void big_step(v4f (&acc)[kWT][NT], BigSmem& sm, XLoad
     __syncthreads();
 }
 
-template <int NT, int S, int s>
-__device__ __forceinline__ void big_group(v4f (&acc)[kWT][NT], BigSmem& sm, XLoader<NT>& xl,
-                                          WStage (&w)[S], const uint8_t* const* wt,
-                                          v8bf (&a0)[kWT], int kb, int KT) {
-    big_step<NT, S, s>(acc, sm, xl, w, wt, a0, kb + s, KT);
-    if constexpr (s + 1 < S) big_group<NT, S, s + 1>(acc, sm, xl, w, wt, a0, kb, KT);
+template <int W, int NT, int S, int s>
+__device__ __forceinline__ void big_group(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
+                                          XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
+                                          const uint8_t* const* wt, v8bf (&a0)[Geo<W>::kWT],
+                                          int kb, int KT) {
+    big_step<W, NT, S, s>(acc, sm, xl, w, wt, a0, kb + s, KT);
+    if constexpr (s + 1 < S) big_group<W, NT, S, s + 1>(acc, sm, xl, w, wt, a0, kb, KT);
+}
+
+// The KT % S remaining k-steps, one guarded step each.
+template <int W, int NT, int S, int r>
+__device__ __forceinline__ void big_tail(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
+                                         XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
+                                         const uint8_t* const* wt, v8bf (&a0)[Geo<W>::kWT],
+                                         int KF, int KT) {
+    if (KF + r < KT) {
+        big_step<W, NT, S, r>(acc, sm, xl, w, wt, a0, KF + r, KT);
+        if constexpr (r + 2 < S) big_tail<W, NT, S, r + 1>(acc, sm, xl, w, wt, a0, KF, KT);
+    }
 }
 
 // Main loop: every wave runs the same KT + 1 barriers.  Activations: LDS
 // double buffer fed from XS register stages.  Weights: S register stages.
 // Whole groups of S k-steps run without any branch; a remainder (only when
 // KT is not a multiple of S) runs through the guarded tail.
-template <int NT>
-__device__ __forceinline__ void big_mainloop(v4f (&acc)[kWT][NT], BigSmem& sm, XLoader<NT>& xl,
-                                             const uint8_t* const* wt, int KT) {
-    constexpr int S = big_stages<NT>();
-    constexpr int XS = XLoader<NT>::XS;
+template <int W, int NT, int S>
+__device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
+                                             XLoader<W, NT>& xl, const uint8_t* const* wt,
+                                             int KT) {
+    constexpr int kWT = Geo<W>::kWT;
+    constexpr int XS = XLoader<W, NT>::XS;
     static_assert(XS == 1 || S % 2 == 0, "two activation stages alternate within a group");
-    WStage w[S];
+    static_assert(S >= 2 && S <= 8, "stages");
+    WStage<kWT> w[S];
 #pragma unroll
     for (int t = 0; t < kWT; ++t)
 #pragma unroll
@@ -224,22 +275,19 @@ __device__ __forceinline__ void big_mainloop(v4f (&acc)[kWT][NT], BigSmem& sm, X
     xl.issue(0, 0);
     if constexpr (XS == 2) xl.issue(min(1, KT - 1), 1);
 #pragma unroll
-    for (int s = 0; s < S - 1; ++s) w_load(w[s], wt, min(s, KT - 1));
+    for (int s = 0; s < S - 1; ++s) w_load<kWT>(w[s], wt, min(s, KT - 1));
     xl.commit(sm, 0, 0, 0);
     __syncthreads();
     v8bf a0[kWT];
     {
-        const uint32_t sc = w_scales(sm, 0);
+        const uint32_t sc = w_scales<kWT>(sm, 0);
 #pragma unroll
-        for (int t = 0; t < kWT; ++t) a0[t] = w_group(w[0], t, 0, scale_of(sc, t));
+        for (int t = 0; t < kWT; ++t) a0[t] = w_group<kWT>(w[0], t, 0, scale_of(sc, t));
     }
     const int KF = KT - KT % S;
 #pragma unroll 1
-    for (int kb = 0; kb < KF; kb += S) big_group<NT, S, 0>(acc, sm, xl, w, wt, a0, kb, KT);
-    if (KF < KT) big_step<NT, S, 0>(acc, sm, xl, w, wt, a0, KF, KT);
-    if (KF + 1 < KT) big_step<NT, S, 1>(acc, sm, xl, w, wt, a0, KF + 1, KT);
-    if constexpr (S > 3)
-        if (KF + 2 < KT) big_step<NT, S, 2>(acc, sm, xl, w, wt, a0, KF + 2, KT);
+    for (int kb = 0; kb < KF; kb += S) big_group<W, NT, S, 0>(acc, sm, xl, w, wt, a0, kb, KT);
+    big_tail<W, NT, S, 0>(acc, sm, xl, w, wt, a0, KF, KT);
 }
 
 // Per-unit context shared by the two kernels.
@@ -281,10 +329,11 @@ __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& i
 // Stages the item's row scales ([k-step][row], 2^0 without x_sf) and the
 // block's 16 weight-tile scales ([k-step][tile], 2^0 without w_sf) in LDS.
 // row_scale(r) points at row r's KT scale bytes; tile_scale(t) at tile t's.
-template <class RowF, class TileF>
+template <int W, class RowF, class TileF>
 __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, bool has_x,
                                                 bool has_w, RowF row_scale, TileF tile_scale) {
-    for (int r = threadIdx.x; r < nrows; r += kBigThreads) {
+    constexpr int T = Geo<W>::kThreads;
+    for (int r = threadIdx.x; r < nrows; r += T) {
         if (has_x) {
             const uint8_t* src = row_scale(r);
             for (int k = 0; k < KT; ++k) sm.sfx[k][r] = src[k];
@@ -292,7 +341,7 @@ __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, 
             for (int k = 0; k < KT; ++k) sm.sfx[k][r] = 127;
         }
     }
-    for (int i = threadIdx.x; i < kBlockTiles * KT; i += kBigThreads) {
+    for (int i = threadIdx.x; i < kBlockTiles * KT; i += T) {
         const int t = i % kBlockTiles, k = i / kBlockTiles;
         sm.sfw[k][t] = has_w ? tile_scale(t)[k] : (uint8_t)127;
     }
@@ -319,55 +368,75 @@ __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, 
 
 // Sets the loader's row offsets: row r of the item (r >= rows: row 0,
 // whose bytes are loaded but whose results are never stored).
-template <int NT, class RowOff>
-__device__ __forceinline__ void big_loader_init(XLoader<NT>& xl, RowOff row_off) {
+template <int W, int NT, class RowOff>
+__device__ __forceinline__ void big_loader_init(XLoader<W, NT>& xl, RowOff row_off) {
+    using XL = XLoader<W, NT>;
 #pragma unroll
-    for (int u = 0; u < XLoader<NT>::U; ++u) {
-        const int i = XLoader<NT>::chunk(u);
-        xl.off[u] = row_off(XLoader<NT>::row_of(i)) + XLoader<NT>::cc_of(i) * 16;
+    for (int u = 0; u < XL::U; ++u) {
+        const int i = XL::chunk(u);
+        xl.off[u] = row_off(XL::row_of(i)) + XL::cc_of(i) * 16;
     }
 }
 
 // ---------------------------------------------------------------------- L1 --
-template <int NT>
+// Block tile bt = kWT*wave + t of an L1 block: the wave's hidden columns are
+// hw0 = bx*128 + wave*(128/W) .. +128/W; tiles t < kWT/2 are the gate rows of
+// columns hw0 + 16t .. +16, tiles t >= kWT/2 the up rows of the same columns
+// (t - kWT/2).  Returns the W1 row of the tile's first row (paired order:
+// gate and up alternate in blocks of G rows).
+template <int W>
+__device__ __forceinline__ int l1_tile_row(int bx, int bt, int G) {
+    constexpr int kWT = Geo<W>::kWT;
+    const int wave = bt / kWT, t = bt % kWT;
+    const int c = t % (kWT / 2), up = t >= kWT / 2;
+    const int hw = bx * kL1BlockH + wave * (kL1BlockH / W) + 16 * c;
+    return (hw / G) * 2 * G + (hw % G) + (up ? G : 0);
+}
+
+template <int W, int NT>
 __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm) {
+    constexpr int kWT = Geo<W>::kWT, kH = kWT / 2;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, G = p.G, KT = H >> 7;
-    XLoader<NT> xl;
+    XLoader<W, NT> xl;
     xl.base = p.x;
-    big_loader_init<NT>(xl, [&](int r) {
+    big_loader_init<W, NT>(xl, [&](int r) {
         const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
         return (p.perm[slot] / (uint32_t)p.topk) * (uint32_t)H;
     });
-    // this wave's 16 hidden columns: gate tile ntg, up tile ntu
-    const int hw = it.bx * kL1BlockH + wave * 16;
-    const int rho = (hw / G) * 2 * G + (hw % G);
-    const int ntg = rho >> 4, ntu = ntg + (G >> 4);
     const uint8_t* we = p.w + (size_t)it.e * (size_t)(2 * I) * H;
     const size_t tstride = (size_t)KT * kTileBytes;
-    const uint8_t* wt[kWT] = {we + (size_t)ntg * tstride + lane * 16,
-                              we + (size_t)ntu * tstride + lane * 16};
+    const uint8_t* wt[kWT];
+#pragma unroll
+    for (int t = 0; t < kWT; ++t)
+        wt[t] = we + (size_t)(l1_tile_row<W>(it.bx, kWT * wave + t, G) >> 4) * tstride + lane * 16;
     v4f acc[kWT][NT];
-    big_mainloop<NT>(acc, sm, xl, wt, KT);
+    big_mainloop<W, NT, big_stages<W, NT, false>()>(acc, sm, xl, wt, KT);
 
-    // h = silu(g) * u: channels hw + 4*(L/16) + i, token 16*j + L%16
-    float hv[NT][4];
+    // h = silu(g) * u: hidden column hw + 16c + 4*(L/16) + i, token 16*j + L%16
+    const int hw = it.bx * kL1BlockH + wave * (kL1BlockH / W);
+    float hv[kH][NT][4];
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int c = 0; c < kH; ++c)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float g = acc[0][j][i], u = acc[1][j][i];
-            hv[j][i] = (g / (1.0f + __expf(-g))) * u;
-        }
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float g = acc[c][j][i], u = acc[c + kH][j][i];
+                hv[c][j][i] = (g / (1.0f + __expf(-g))) * u;
+            }
     const int I128 = I >> 7;
     if (p.ffn_ue8m0) {
-        // amax over the block's 128 hidden columns = the 8 waves; the LDS
+        // amax over the block's 128 hidden columns = the W waves; the LDS
         // tiles are free after the main loop's last barrier.
-        float* red = reinterpret_cast<float*>(&sm.x[0][0]);   // [8][kBigRows]
+        float* red = reinterpret_cast<float*>(&sm.x[0][0]);   // [W][kBigRows]
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            float m = fmaxf(fmaxf(fabsf(hv[j][0]), fabsf(hv[j][1])),
-                            fmaxf(fabsf(hv[j][2]), fabsf(hv[j][3])));
+            float m = 0.0f;
+#pragma unroll
+            for (int c = 0; c < kH; ++c)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(hv[c][j][0]), fabsf(hv[c][j][1])),
+                                   fmaxf(fabsf(hv[c][j][2]), fabsf(hv[c][j][3]))));
             m = fmaxf(m, __shfl_xor(m, 16, 64));
             m = fmaxf(m, __shfl_xor(m, 32, 64));
             if (lane < 16) red[wave * kBigRows + 16 * j + lane] = m;
@@ -378,13 +447,16 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
             const int r = 16 * j + (lane & 15);
             float amax = red[r];
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w) amax = fmaxf(amax, red[w * kBigRows + r]);
+            for (int w = 1; w < W; ++w) amax = fmaxf(amax, red[w * kBigRows + r]);
             const uint32_t sb = block_scale_byte(amax);
             const float inv = inv_scale(sb);
             if (r < it.rows) {
                 const size_t slot = (size_t)(it.off + it.m0 + r);
-                *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 4 * (lane >> 4)) =
-                    pack4_fp8(hv[j][0] * inv, hv[j][1] * inv, hv[j][2] * inv, hv[j][3] * inv);
+#pragma unroll
+                for (int c = 0; c < kH; ++c)
+                    *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4)) =
+                        pack4_fp8(hv[c][j][0] * inv, hv[c][j][1] * inv, hv[c][j][2] * inv,
+                                  hv[c][j][3] * inv);
                 if (wave == 0 && lane < 16) p.out_sf[slot * I128 + it.bx] = (uint8_t)sb;
             }
         }
@@ -394,8 +466,10 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
             const int r = 16 * j + (lane & 15);
             if (r < it.rows) {
                 const size_t slot = (size_t)(it.off + it.m0 + r);
-                *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 4 * (lane >> 4)) =
-                    pack4_fp8(hv[j][0], hv[j][1], hv[j][2], hv[j][3]);
+#pragma unroll
+                for (int c = 0; c < kH; ++c)
+                    *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4)) =
+                        pack4_fp8(hv[c][j][0], hv[c][j][1], hv[c][j][2], hv[c][j][3]);
             }
         }
     }
@@ -403,47 +477,50 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
 
 // NT (the item's token tiles) is uniform over the block, so every wave runs
 // the same body and the same barriers.
-__global__ void __launch_bounds__(kBigThreads) l1_big_kernel(GemmParams p) {
+template <int W>
+__device__ __forceinline__ void l1_big(const GemmParams& p) {
     __shared__ BigSmem sm;
     BigItem it;
     if (!big_unit(p, p.I / kL1BlockH, it)) return;
     const int KT = p.H >> 7, I = p.I, G = p.G;
     const int tiles = (it.rows + 15) >> 4;
-    // scales: x rows through perm[]; W1 tiles 2*wave (gate), 2*wave+1 (up)
-    big_load_scales(
+    // scales: x rows through perm[]; W1 tiles as l1_tile_row places them
+    big_load_scales<W>(
         sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
         [&](int r) {
             const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
             return p.x_sf + (size_t)(p.perm[slot] / (uint32_t)p.topk) * KT;
         },
         [&](int t) {
-            const int hw = it.bx * kL1BlockH + (t >> 1) * 16;
-            const int rho = (hw / G) * 2 * G + (hw % G) + ((t & 1) ? G : 0);
+            const int rho = l1_tile_row<W>(it.bx, t, G);
             return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
         });
-#define MM_L1_BODY(n) l1_big_body<n>(p, it, sm)
+#define MM_L1_BODY(n) l1_big_body<W, n>(p, it, sm)
     MM_BIG_DISPATCH(MM_L1_BODY)
 #undef MM_L1_BODY
 }
 
+__global__ void __launch_bounds__(512) l1_big_kernel(GemmParams p) { l1_big<8>(p); }
+
 // ---------------------------------------------------------------------- L2 --
-template <int NT>
+template <int W, int NT>
 __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm) {
+    constexpr int kWT = Geo<W>::kWT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, KT = I >> 7;
-    XLoader<NT> xl;
+    XLoader<W, NT> xl;
     xl.base = p.x;
-    big_loader_init<NT>(xl, [&](int r) {
+    big_loader_init<W, NT>(xl, [&](int r) {
         return (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
     });
-    const int n0 = it.bx * kL2BlockN + wave * 32;   // this wave's 32 output channels
+    const int n0 = it.bx * kL2BlockN + wave * (kL2BlockN / W);   // the wave's output channels
     const uint8_t* we = p.w + (size_t)it.e * (size_t)H * I;
     const size_t tstride = (size_t)KT * kTileBytes;
     const uint8_t* wt[kWT];
 #pragma unroll
     for (int t = 0; t < kWT; ++t) wt[t] = we + (size_t)((n0 >> 4) + t) * tstride + lane * 16;
     v4f acc[kWT][NT];
-    big_mainloop<NT>(acc, sm, xl, wt, KT);
+    big_mainloop<W, NT, big_stages<W, NT, true>()>(acc, sm, xl, wt, KT);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         const int r = 16 * j + (lane & 15);
@@ -460,24 +537,27 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     }
 }
 
-__global__ void __launch_bounds__(kBigThreads) l2_big_kernel(GemmParams p) {
+template <int W>
+__device__ __forceinline__ void l2_big(const GemmParams& p) {
     __shared__ BigSmem sm;
     BigItem it;
     if (!big_unit(p, p.H / kL2BlockN, it)) return;
     const int KT = p.I >> 7, H = p.H;
     const int tiles = (it.rows + 15) >> 4;
     // scales: ffn rows in slot order; W2 tiles of this block's 256 channels
-    big_load_scales(
+    big_load_scales<W>(
         sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
         [&](int r) { return p.x_sf + (size_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * KT; },
         [&](int t) {
             const int n = it.bx * kL2BlockN + t * 16;
             return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
         });
-#define MM_L2_BODY(n) l2_big_body<n>(p, it, sm)
+#define MM_L2_BODY(n) l2_big_body<W, n>(p, it, sm)
     MM_BIG_DISPATCH(MM_L2_BODY)
 #undef MM_L2_BODY
 }
+
+__global__ void __launch_bounds__(512) l2_big_kernel(GemmParams p) { l2_big<8>(p); }
 
 #undef MM_BIG_DISPATCH
 
