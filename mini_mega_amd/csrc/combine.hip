@@ -5,7 +5,10 @@
 // in fp32, product then add (no fused multiply-add, so the sum is bitwise the
 // reference's sequential loop); pairs without a slot (invalid expert id or
 // over the slot cap) contribute nothing.  Each thread owns 8 channels (one
-// 16-byte bf16 load per k), no atomics: the output is deterministic.
+// 16-byte bf16 load per k), no atomics: the output is deterministic.  The
+// k-loop runs in groups of 8 whose slot indices, weights and row loads are
+// all issued before the group's in-order accumulation, so a thread waits for
+// one memory latency per group instead of one per k.
 #include "mm_kernels.h"
 
 namespace mm {
@@ -15,24 +18,40 @@ combine_kernel(const uint16_t* __restrict__ l2, const int* __restrict__ pair_pos
                const float* __restrict__ w, int topk, int H, float* __restrict__ y,
                uint16_t* __restrict__ y_bf16) {
 #pragma clang fp contract(off)
+    constexpr int kG = 8;
     const int t = blockIdx.x;
     const int c0 = (blockIdx.y * blockDim.x + threadIdx.x) * 8;
     if (c0 >= H) return;
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int k = 0; k < topk; ++k) {
-        const int pos = pair_pos[(size_t)t * topk + k];
-        if (pos < 0) continue;
-        const float wv = w[(size_t)t * topk + k];
-        const v4i raw = load16(reinterpret_cast<const uint8_t*>(l2 + (size_t)pos * H + c0));
+    const int* pp = pair_pos + (size_t)t * topk;
+    const float* ww = w + (size_t)t * topk;
+    for (int k0 = 0; k0 < topk; k0 += kG) {
+        int pos[kG];
+        float wv[kG];
+        v4i raw[kG];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t u = (uint32_t)raw[i];
-            const float lo = bf16_to_f32(u & 0xFFFFu) * wv;
-            const float hi = bf16_to_f32(u >> 16) * wv;
-            acc[2 * i] = acc[2 * i] + lo;
-            acc[2 * i + 1] = acc[2 * i + 1] + hi;
+        for (int j = 0; j < kG; ++j) {
+            pos[j] = k0 + j < topk ? pp[k0 + j] : -1;
+            wv[j] = k0 + j < topk ? ww[k0 + j] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kG; ++j)
+            raw[j] = pos[j] >= 0
+                         ? load16(reinterpret_cast<const uint8_t*>(l2 + (size_t)pos[j] * H + c0))
+                         : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < kG; ++j) {
+            if (pos[j] < 0) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t u = (uint32_t)raw[j][i];
+                const float lo = bf16_to_f32(u & 0xFFFFu) * wv[j];
+                const float hi = bf16_to_f32(u >> 16) * wv[j];
+                acc[2 * i] = acc[2 * i] + lo;
+                acc[2 * i + 1] = acc[2 * i + 1] + hi;
+            }
         }
     }
     if (y) {
