@@ -105,7 +105,8 @@ struct MegaLaunchArgs {
 // counterpart of mt::make_geo / compute_layout, test/mega_common.cuh:69-88,
 // src/host_layout.cuh:59-100).  All offsets are 256-byte aligned.
 struct MegaLayout {
-    int64_t status;        // int32[16]: [0] status word, [1] items, [2] slots
+    int64_t status;        // int32[64]: [0] status word, [1] items, [2] slots,
+                           // [16..24] / [32..40] XCD unit ranges of the L1 / L2 GEMMs
     int64_t chunk_hist;    // int32[nchunks][E] per-chunk histograms -> prefixes
     int64_t counts;        // int32[E]   per-expert routed rows (after cap)
     int64_t offsets;       // int32[E+1] exclusive prefix of counts

@@ -302,16 +302,15 @@ struct BigItem {
 // at the same time, so all but one take the block from that XCD's L2.  (The
 // expert of unit u is the one of item u / nb: its items are consecutive.)
 // The XCDs take workgroups round-robin, so workgroup L (the k-th of XCD L%8,
-// k = L/8) runs unit (L%8)*c + k with c = ceil(units / 8): each XCD walks a
-// contiguous range.  The grid has nb * max_items + 8 workgroups, enough for
-// 8*c; the surplus exits.
+// k = L/8) runs unit xcd_cuts[L%8] + k: each XCD walks a contiguous range,
+// the ranges cut by the routing scan at equal modelled cost (skewed routing
+// mixes units of 1 and 16 token tiles).  The grid has nb * max_items + 8
+// workgroups, at least 8 times the longest range; the surplus exits.
 __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& it) {
-    const int units = nb * p.status[1];
-    const int c = (units + 7) >> 3;
     const int L = blockIdx.x;
-    const int k = L >> 3;
-    const int u = (L & 7) * c + k;
-    if (k >= c || u >= units) return false;
+    const int x = L & 7, k = L >> 3;
+    const int u = p.xcd_cuts[x] + k;
+    if (u >= p.xcd_cuts[x + 1]) return false;
     const int4* items = reinterpret_cast<const int4*>(p.items);
     const int im = u / nb;                 // item-major item: same expert
     const int jn = items[im].w;

@@ -20,15 +20,17 @@ thread_local int g_last_error = kOk;
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
 int auto_m_tile(int tokens, int topk, int E) {
-    // Rows per work item: one item per expert when the expected expert load
-    // (plus the spread of a random router) fits, so that each expert's weights
-    // stream from HBM once.  The LDS-staged 8-wave kernels (64..256 rows) are
-    // at least as fast as the decode-shaped ones (win_cap 16/32) from T = 512
-    // (measured on MI355X: L1 955 vs 1003 us, L2 568 vs 591 us), so the
-    // automatic choice always uses them.
-    const double mean = (double)tokens * topk / (E > 0 ? E : 1);
-    if (mean <= 44.0) return 64;
-    if (mean <= 96.0) return 128;
+    // Rows per work item: the largest window of the LDS-staged kernels (256),
+    // so that an expert's weights stream from HBM once whenever its load fits
+    // and a hot expert splits into as few items as possible.  Measured on
+    // MI355X (L1 / L2 us): balanced routing gives the same items for every
+    // window up to T = 2048; T = 4096: 1783 / 986 vs 1960 / 1079 with 128;
+    // T = 8192: 3363 / 1813 vs 3406 / 1845 with 128; Zipf(1.1) T = 1024: 960 /
+    // 554 vs 1000 / 585 with 64, T = 2048: 1240 / 682 vs 1277 / 701 with 128.
+    // The decode-shaped kernels (win_cap 16/32) are slower from T = 512 on.
+    (void)tokens;
+    (void)topk;
+    (void)E;
     return 16 * mm::kBigMaxTiles;
 }
 
@@ -109,7 +111,8 @@ int do_prelude(const MegaLaunchArgs& a, hipStream_t s) {
                            a.topk_idx, P, E, hist);
     const int cap = a.slot_capacity > 0 ? a.slot_capacity : (P > 0 ? P : 1);
     hipLaunchKernelGGL(mm::route_scan_kernel, dim3(1), dim3(mm::kScanThreads), 0, s, hist,
-                       nchunks, E, cap, b.m_tile, b.L.max_items, at<int>(b, b.L.counts),
+                       nchunks, E, cap, b.m_tile, b.L.max_items, a.intermediate / mm::kL1BlockH,
+                       a.hidden / mm::kL2BlockN, at<int>(b, b.L.counts),
                        at<int>(b, b.L.offsets), at<int>(b, b.L.items), status);
     int nbits = 0;
     while ((1 << nbits) < E) ++nbits;
@@ -166,6 +169,7 @@ int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     p.w_sf = a.w1_sf;
     p.out8 = b.ws + b.L.ffn;
     p.out_sf = b.ws + b.L.ffn_sf;
+    p.xcd_cuts = p.status + mm::kCutsL1;
     const int nb = a.intermediate / mm::kL1BlockH;
     launch_gemm(kL1Small, mm::l1_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
@@ -182,6 +186,7 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     p.w = a.w2;
     p.w_sf = a.w2_sf;
     p.out16 = at<uint16_t>(b, b.L.l2);
+    p.xcd_cuts = p.status + mm::kCutsL2;
     const int nb = a.hidden / mm::kL2BlockN;
     launch_gemm(kL2Small, mm::l2_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
@@ -250,7 +255,7 @@ MegaLayout layout(int max_tokens, int topk, int num_experts, int hidden, int int
     L.m_tile = win_cap > 0 ? win_cap : auto_m_tile(max_tokens, topk, num_experts);
     L.max_items = (int)((P + L.m_tile - 1) / L.m_tile + E);
     int64_t o = 0;
-    L.status = o;      o = align256(o + 16 * 4);
+    L.status = o;      o = align256(o + mm::kStatusInts * 4);
     L.chunk_hist = o;  o = align256(o + (int64_t)L.nchunks * E * 4);
     L.counts = o;      o = align256(o + E * 4);
     L.offsets = o;     o = align256(o + (E + 1) * 4);

@@ -18,6 +18,9 @@ constexpr int kBigMaxTiles = 16;    // large-M GEMMs: up to 16 token tiles (256 
 constexpr int kBigMaxKT = 64;       // large-M GEMMs: K / 128 <= 64 (H, I <= 8192)
 constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 workgroup
 constexpr int kL2BlockN = 256;      // output channels per L2 workgroup
+constexpr int kStatusInts = 64;     // workspace status words
+constexpr int kCutsL1 = 16;         // status[16..24]: XCD unit ranges of the L1 big GEMM
+constexpr int kCutsL2 = 32;         // status[32..40]: the same for L2
 
 // Parameters of the two grouped GEMMs (one struct so that the launcher and
 // the kernels agree on one argument list).
@@ -31,6 +34,7 @@ struct GemmParams {
     const int* items;         // [max_items][4]: expert, first row, end row, j | n << 16
                               // (item j of the expert's n)
     const int* status;        // [1] = number of items
+    const int* xcd_cuts;      // [9]: XCD x runs big-GEMM units [cuts[x], cuts[x+1])
     const uint32_t* perm;     // slot -> pair (L1 gathers x rows through it)
     uint8_t* out8;            // L1: ffn fp8 [P][I]
     uint8_t* out_sf;          // L1: ffn scales [P][I/128] (ffn_ue8m0)
@@ -45,7 +49,7 @@ __global__ void l1_big_kernel(GemmParams p);
 __global__ void l2_big_kernel(GemmParams p);
 
 __global__ void route_hist_kernel(const int64_t*, int, int, int*);
-__global__ void route_scan_kernel(int*, int, int, int, int, int, int*, int*, int*, int*);
+__global__ void route_scan_kernel(int*, int, int, int, int, int, int, int, int*, int*, int*, int*);
 __global__ void route_scatter_kernel(const int64_t*, int, int, int, const int*, const int*,
                                      const int*, uint32_t*, int*);
 __global__ void dispatch_gather_kernel(const uint8_t*, int, int, const uint32_t*, const int*,

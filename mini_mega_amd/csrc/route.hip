@@ -64,9 +64,10 @@ __device__ int block_exclusive_scan(int v, int* smem, int* total) {
 
 __global__ void __launch_bounds__(kScanThreads)
 route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int m_tile,
-                  int max_items, int* __restrict__ counts, int* __restrict__ offsets,
-                  int* __restrict__ items, int* __restrict__ status) {
+                  int max_items, int nb1, int nb2, int* __restrict__ counts,
+                  int* __restrict__ offsets, int* __restrict__ items, int* __restrict__ status) {
     __shared__ int smem[kScanThreads / 64 + 1];
+    __shared__ int cut_s[2][8];
     // E <= kMaxExperts = kScanThreads: one expert per thread.
     const int e = threadIdx.x;
     int cnt = 0;
@@ -104,6 +105,48 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
         status[1] = min(nitems, max_items);
         status[2] = slots;
         if (nitems > max_items) atomicOr(&status[0], 1);
+    }
+    // XCD ranges of the big GEMMs' units (nb blocks per item; an expert's
+    // nb * nm units are contiguous in the kernels' numbering).  Modelled cost
+    // of one of the expert's units per k-step, in token-tile MFMA times:
+    // max(9, 2 + token tiles of its largest item) -- the fixed per-step work
+    // (barrier, conversions, operand reads) is worth ~2 token tiles and the
+    // weight stream at the full-chip HBM rate ~9 (measured on MI355X: a
+    // k-step costs ~0.33 us + 0.137 us per token tile without weight loads,
+    // and a weight block's k-step streams in ~1.23 us).  XCD x starts where
+    // the running cost crosses x/8 of the total (the same expert for L1 and
+    // L2, whose costs differ by the factor nb); each range is then clamped to
+    // its share of the grid, nb * max_items + 8 workgroups.
+    const int uc = max(9, 2 + min((sz + 15) >> 4, kBigMaxTiles));
+    const int w = nm * uc;
+    int wtot = 0;
+    const int wpre = block_exclusive_scan(w, smem, &wtot);
+    if (nm > 0 && ioff + nm <= max_items) {
+        for (int x = 1; x < 8; ++x) {
+            const int64_t t1 = (int64_t)wtot * nb1 * x / 8, t2 = (int64_t)wtot * nb2 * x / 8;
+            const int64_t lo1 = (int64_t)wpre * nb1, lo2 = (int64_t)wpre * nb2;
+            if (t1 >= lo1 && t1 < lo1 + (int64_t)w * nb1)
+                cut_s[0][x] = nb1 * ioff + (int)((t1 - lo1) / uc);
+            if (t2 >= lo2 && t2 < lo2 + (int64_t)w * nb2)
+                cut_s[1][x] = nb2 * ioff + (int)((t2 - lo2) / uc);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        const int nb = threadIdx.x == 0 ? nb1 : nb2;
+        const int n = min(nitems, max_items), units = nb * n, cap = (nb * max_items + 8) / 8;
+        int* cuts = status + (threadIdx.x == 0 ? kCutsL1 : kCutsL2);
+        int prev = 0;
+        cuts[0] = 0;
+        for (int x = 1; x < 8; ++x) {
+            // a target past the last complete expert (item overflow) cuts at the end
+            int v = nitems <= max_items && n > 0 ? cut_s[threadIdx.x][x] : units;
+            v = min(max(v, prev), prev + cap);
+            v = max(v, units - (8 - x) * cap);
+            cuts[x] = v;
+            prev = v;
+        }
+        cuts[8] = units;
     }
 }
 

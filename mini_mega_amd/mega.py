@@ -157,7 +157,7 @@ class SymmBuffer:
         return self._ws(self.layout.l2, torch.int16, (slots, self.hidden))
 
     def status(self):
-        return self._ws(self.layout.status, torch.int32, (16,))
+        return self._ws(self.layout.status, torch.int32, (64,))
 
     def items(self, n: int):
         """Work items: (expert, first row, end row, j | n << 16 for item j of

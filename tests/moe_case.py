@@ -133,6 +133,49 @@ def check_routing(c: Case, r: Run):
     assert int(r.status[1]) == len(want), "work item count differs"
     got = r.buf.items(len(want)).cpu().numpy() if want else np.zeros((0, 4), np.int32)
     assert np.array_equal(got, np.array(want, dtype=np.int32).reshape(-1, 4)), "work items differ"
+    # XCD unit ranges of the big GEMMs (status[16..24] for L1, [32..40] for L2)
+    max_items = int(r.buf.layout.max_items)
+    for base, nb in ((16, c.I // 128), (32, c.H // 256)):
+        cuts = np.asarray(r.status[base:base + 9]).astype(np.int64)
+        assert np.array_equal(cuts, xcd_cuts(counts, m_tile, nb, max_items)), \
+            f"XCD unit ranges differ (nb={nb})"
+
+
+def xcd_cuts(counts, m_tile, nb, max_items):
+    """The routing scan's XCD ranges, restated: expert e's nb * nm units (nm
+    items of at most sz rows) each cost max(9, 2 + token tiles of sz); XCD x
+    starts where the running cost crosses x/8 of the total, and every range
+    is clamped to the grid's share (nb * max_items + 8) // 8."""
+    nms, ucs = [], []
+    for cnt in np.asarray(counts).tolist():
+        nm = -(-cnt // m_tile)
+        sz = -(-cnt // nm) if nm else 0
+        nms.append(nm)
+        ucs.append(max(9, 2 + min((sz + 15) // 16, 16)))
+    n = sum(nms)
+    total = sum(nm * uc for nm, uc in zip(nms, ucs))
+    raw = [0] * 8
+    ioff = pre = 0
+    for nm, uc in zip(nms, ucs):
+        w = nm * uc
+        lo, hi = pre * nb, (pre + w) * nb
+        for x in range(1, 8):
+            tgt = total * nb * x // 8
+            if nm and lo <= tgt < hi:
+                raw[x] = nb * ioff + (tgt - lo) // uc
+        ioff += nm
+        pre += w
+    units = nb * min(n, max_items)
+    cap = (nb * max_items + 8) // 8
+    cuts, prev = [0], 0
+    for x in range(1, 8):
+        v = raw[x] if 0 < n <= max_items else units
+        v = min(max(v, prev), prev + cap)
+        v = max(v, units - (8 - x) * cap)
+        cuts.append(v)
+        prev = v
+    cuts.append(units)
+    return np.array(cuts, dtype=np.int64)
 
 
 def _bad(got, want, rel, abs_tol):

@@ -102,3 +102,26 @@ def test_paired_row_map_is_reference_pairing(I):
     for h in sorted({0, 1, G - 1, min(G, I - 1), I - 1}):
         assert m[(h // G) * 2 * G + h % G] == h
         assert m[(h // G) * 2 * G + h % G + G] == I + h
+
+
+def test_xcd_ranges_partition_units_and_balance_cost():
+    """The XCD unit ranges the routing scan computes (restated in moe_case.xcd_cuts):
+    a partition of the units into 8 contiguous ranges, each within its share of
+    the grid, with modelled costs equal to within one expert's units."""
+    import moe_case as mc
+    rng = np.random.default_rng(7)
+    for E, mean, m_tile, nb in ((8, 20, 64, 16), (256, 16, 256, 24), (256, 256, 256, 16),
+                                (256, 64, 128, 24)):
+        counts = rng.poisson(mean, size=E)
+        counts[rng.integers(0, E)] *= 6   # one hot expert
+        nm = -(-counts // m_tile)
+        max_items = int(counts.sum() // m_tile + E)
+        cuts = mc.xcd_cuts(counts, m_tile, nb, max_items)
+        units = nb * int(nm.sum())
+        assert cuts[0] == 0 and cuts[-1] == units and np.all(np.diff(cuts) >= 0)
+        assert np.all(np.diff(cuts) <= (nb * max_items + 8) // 8)
+        sz = np.where(nm > 0, -(-counts // np.maximum(nm, 1)), 0)
+        uc = np.maximum(9, 2 + np.minimum((sz + 15) // 16, 16))
+        cost = np.repeat(uc, nb * nm)
+        per = np.array([cost[a:b].sum() for a, b in zip(cuts[:-1], cuts[1:])])
+        assert per.max() - per.min() <= 2 * 18 + 1, per
