@@ -127,6 +127,8 @@ class SymmBuffer:
         self._x_off, self._w_off = x_off, w_off
         self.workspace = torch.zeros(int(self.layout.total), dtype=torch.uint8, device="cuda")
         self._y_fp32 = torch.empty((cap, self.hidden), dtype=torch.float32, device="cuda")
+        # also write the fp32 y next to a bf16 output (staged checks read it)
+        self.write_fp32_y = False
         self.launch_count = 0
 
     # -- workspace views (staged parity checks read these, as check.cu dumps
@@ -183,7 +185,14 @@ class SymmBuffer:
         a.w1 = w1.data_ptr()
         a.w2 = w2.data_ptr()
         a.in_bf16 = 1 if self.mma_type == "bf16xfp8" else 0
-        a.y = (y_fp32 if y_fp32 is not None else self._y_fp32).data_ptr()
+        # fp32 y (the reference's MegaLaunchArgs::y) only when asked for, or
+        # when there is no bf16 output: it is 4*T*H more bytes to write
+        if y_fp32 is not None:
+            a.y = y_fp32.data_ptr()
+        elif self.write_fp32_y or y_bf16 is None:
+            a.y = self._y_fp32.data_ptr()
+        else:
+            a.y = None
         a.y_bf16 = y_bf16.data_ptr() if y_bf16 is not None else None
         a.skip_prologue = int(skip_prologue)
         a.num_experts, a.topk = self.num_experts, self.num_topk

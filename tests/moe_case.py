@@ -96,6 +96,7 @@ class Run:
 
 def run_layer(c: Case, skip_fetch_l2: bool = False) -> Run:
     buf = mm.get_symm_buffer_for_mega_moe(None, c.E, c.T, c.K, c.H, c.I, expert_window=c.win)
+    buf.write_fp32_y = True
     buf.x.view(torch.uint8)[:c.T].copy_(torch.from_numpy(c.x))
     if c.xsf is not None:
         buf.x_sf[:c.T].copy_(torch.from_numpy(c.xsf))

@@ -255,6 +255,7 @@ def test_layer_bf16_input_fold():
     (w1, s1), (w2, s2) = inputs.make_weights_normal(E, H, I, seed=6)
     idx, wts = inputs.route(T, E, K, seed=7)
     buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I, mma_type="bf16xfp8")
+    buf.write_fp32_y = True
     buf.x[:T].copy_(xb)
     buf.topk_idx[:T].copy_(torch.from_numpy(idx))
     buf.topk_weights[:T].copy_(torch.from_numpy(wts))
