@@ -119,7 +119,7 @@ struct MegaLayout {
     int64_t ffn_sf;        // uint8[P][I/128] L1 output scales
     int64_t l2;            // uint16[P][H]  L2 output (bf16, slot order)
     int64_t total;         // bytes
-    int nchunks;           // routing chunks (1024 pairs each)
+    int nchunks;           // routing chunk histograms held (256 pairs each up to 8192 pairs, 1024 above)
     int max_items;         // upper bound on work items for the chosen M tile
     int max_pairs;         // P = max_tokens * topk
     int m_tile;            // rows per work item

@@ -104,11 +104,12 @@ int do_prelude(const MegaLaunchArgs& a, hipStream_t s) {
                                a.tokens, a.hidden, b.ws + b.L.xq,
                                a.w1_sf ? b.ws + b.L.xq_sf : nullptr);
     }
-    const int nchunks = P > 0 ? (P + mm::kRouteChunk - 1) / mm::kRouteChunk : 0;
+    const int chunk = mm::route_chunk(P);
+    const int nchunks = P > 0 ? (P + chunk - 1) / chunk : 0;
     int* hist = at<int>(b, b.L.chunk_hist);
     if (nchunks > 0)
         hipLaunchKernelGGL(mm::route_hist_kernel, dim3(nchunks), dim3(mm::kRouteThreads), 0, s,
-                           a.topk_idx, P, E, hist);
+                           a.topk_idx, P, E, chunk, hist);
     const int cap = a.slot_capacity > 0 ? a.slot_capacity : (P > 0 ? P : 1);
     hipLaunchKernelGGL(mm::route_scan_kernel, dim3(1), dim3(mm::kScanThreads), 0, s, hist,
                        nchunks, E, cap, b.m_tile, b.L.max_items, a.intermediate / mm::kL1BlockH,
@@ -118,7 +119,7 @@ int do_prelude(const MegaLaunchArgs& a, hipStream_t s) {
     while ((1 << nbits) < E) ++nbits;
     if (nchunks > 0)
         hipLaunchKernelGGL(mm::route_scatter_kernel, dim3(nchunks), dim3(mm::kRouteThreads), 0,
-                           s, a.topk_idx, P, E, nbits, hist, at<int>(b, b.L.counts),
+                           s, a.topk_idx, P, E, nbits, chunk, hist, at<int>(b, b.L.counts),
                            at<int>(b, b.L.offsets), at<uint32_t>(b, b.L.perm),
                            at<int>(b, b.L.pair_pos));
     return launched(kOk);
@@ -251,7 +252,11 @@ MegaLayout layout(int max_tokens, int topk, int num_experts, int hidden, int int
     const int64_t P = (int64_t)(max_tokens > 0 ? max_tokens : 1) * topk;
     const int64_t E = num_experts;
     L.max_pairs = (int)P;
-    L.nchunks = (int)((P + mm::kRouteChunk - 1) / mm::kRouteChunk);
+    // room for the per-chunk histograms of any launch up to P pairs
+    const int64_t ps = P < mm::kRouteSmallP ? P : mm::kRouteSmallP;
+    const int64_t n_small = (ps + mm::kRouteChunkSmall - 1) / mm::kRouteChunkSmall;
+    const int64_t n_large = (P + mm::kRouteChunkLarge - 1) / mm::kRouteChunkLarge;
+    L.nchunks = (int)(n_small > n_large ? n_small : n_large);
     L.m_tile = win_cap > 0 ? win_cap : auto_m_tile(max_tokens, topk, num_experts);
     L.max_items = (int)((P + L.m_tile - 1) / L.m_tile + E);
     int64_t o = 0;

@@ -19,13 +19,13 @@
 namespace mm {
 
 __global__ void __launch_bounds__(kRouteThreads)
-route_hist_kernel(const int64_t* __restrict__ topk_idx, int P, int E,
+route_hist_kernel(const int64_t* __restrict__ topk_idx, int P, int E, int chunk,
                   int* __restrict__ chunk_hist) {
     __shared__ int hist[kMaxExperts];
     for (int i = threadIdx.x; i < E; i += blockDim.x) hist[i] = 0;
     __syncthreads();
-    const int base = blockIdx.x * kRouteChunk;
-    const int end = min(base + kRouteChunk, P);
+    const int base = blockIdx.x * chunk;
+    const int end = min(base + chunk, P);
     for (int p = base + threadIdx.x; p < end; p += blockDim.x) {
         const int64_t e = topk_idx[p];
         if (e >= 0 && e < E) atomicAdd(&hist[(int)e], 1);
@@ -72,12 +72,20 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
     const int e = threadIdx.x;
     int cnt = 0;
     if (e < E) {
+        // exclusive prefix over chunks (uncapped rank base), 8 chunks' loads
+        // in flight at a time
         int run = 0;
-        for (int c = 0; c < nchunks; ++c) {
-            const size_t i = (size_t)c * E + e;
-            const int h = chunk_hist[i];
-            chunk_hist[i] = run;  // exclusive prefix over chunks (uncapped rank base)
-            run += h;
+        for (int c0 = 0; c0 < nchunks; c0 += 8) {
+            int h[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                h[u] = c0 + u < nchunks ? chunk_hist[(size_t)(c0 + u) * E + e] : 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (c0 + u < nchunks) {
+                    chunk_hist[(size_t)(c0 + u) * E + e] = run;
+                    run += h[u];
+                }
         }
         cnt = min(run, cap);
         counts[e] = cnt;
@@ -151,7 +159,7 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
 }
 
 __global__ void __launch_bounds__(kRouteThreads)
-route_scatter_kernel(const int64_t* __restrict__ topk_idx, int P, int E, int nbits,
+route_scatter_kernel(const int64_t* __restrict__ topk_idx, int P, int E, int nbits, int chunk,
                      const int* __restrict__ chunk_hist, const int* __restrict__ counts,
                      const int* __restrict__ offsets, uint32_t* __restrict__ perm,
                      int* __restrict__ pair_pos) {
@@ -165,9 +173,9 @@ route_scatter_kernel(const int64_t* __restrict__ topk_idx, int P, int E, int nbi
         for (int w = 0; w < kWaves; ++w) cntw[w][i] = 0;
     }
     __syncthreads();
-    const int base = blockIdx.x * kRouteChunk;
+    const int base = blockIdx.x * chunk;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int r0 = base; r0 < min(base + kRouteChunk, P); r0 += kRouteThreads) {
+    for (int r0 = base; r0 < min(base + chunk, P); r0 += kRouteThreads) {
         const int p = r0 + threadIdx.x;
         const bool in = p < P;
         const int64_t e64 = in ? topk_idx[p] : -1;
