@@ -231,6 +231,32 @@ SMALL = [
 ]
 
 
+def test_every_token_tile_count():
+    """Expert e gets 16(e+1) - 3 rows, so one 256-row window runs each of the
+    big GEMMs' token-tile specialisations (1..8, then 10, 12, 14, 16 for the
+    odd counts above 8) on at least one item; every expert is checked staged."""
+    E, K, H, I = 16, 8, 512, 256
+    rows = [16 * (e + 1) - 3 for e in range(E)]
+    ids = np.repeat(np.arange(E), rows)
+    rng = np.random.default_rng(21)
+    rng.shuffle(ids)
+    T = ids.size // K
+    idx = ids[:T * K].reshape(T, K).astype(np.int64)
+    wts = rng.random((T, K)).astype(np.float32)
+    wts /= wts.sum(axis=1, keepdims=True)
+    _say(f"every token-tile count T={T}")
+    c = mc.normal_case(E, K, H, I, T, seed=31, scaled=True, idx=idx, wts=wts)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    assert int(r.buf.layout.m_tile) == 256
+    for e in range(E):
+        mc.check_l1(c, r, e, max_rows=256)
+        mc.check_l2(c, r, e, max_rows=256)
+    mc.check_reduce(c, r)
+    err, rms, cos = mc.check_e2e_tokens(c, r, [0, 1, T // 2, T - 1])
+    _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
 @pytest.mark.parametrize("E,K,H,I,T,scaled,win", SMALL)
 def test_layer_staged_and_e2e(E, K, H, I, T, scaled, win):
     _say(f"layer E={E} K={K} H={H} I={I} T={T} scaled={scaled} win={win}")
