@@ -94,8 +94,7 @@ int do_prelude(const MegaLaunchArgs& a, hipStream_t s) {
     int st = bind(a, b, false);
     if (st != kOk) return st;
     const int E = a.num_experts, P = a.tokens * a.topk;
-    int* status = at<int>(b, b.L.status);
-    hipLaunchKernelGGL(mm::fill_int_kernel, dim3(1), dim3(256), 0, s, status, 16, 0);
+    int* status = at<int>(b, b.L.status);   // reset and written by route_scan_kernel
     if (a.in_bf16) {
         const size_t n8 = (size_t)a.tokens * a.hidden / 8;
         if (n8 > 0)

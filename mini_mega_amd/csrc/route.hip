@@ -68,6 +68,9 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
                   int* __restrict__ offsets, int* __restrict__ items, int* __restrict__ status) {
     __shared__ int smem[kScanThreads / 64 + 1];
     __shared__ int cut_s[2][8];
+    // the status word of this launch (only this kernel sets its error bits;
+    // thread 0 clears it before its own atomicOr below)
+    if (threadIdx.x == 0) status[0] = 0;
     // E <= kMaxExperts = kScanThreads: one expert per thread.
     const int e = threadIdx.x;
     int cnt = 0;
