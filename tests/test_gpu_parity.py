@@ -228,6 +228,7 @@ SMALL = [
     (8, 8, 256, 128, 300, True, 128),    # every token routed to every expert: 3 items each
     (8, 8, 256, 128, 250, True, 256),    # 250 rows per expert: one item of 16 token tiles
     (24, 6, 1024, 512, 700, True, 0),    # auto tile: 175 rows per expert -> one 256-row window
+    (16, 4, 7168, 1280, 200, True, 0),   # H = 7168 (56 k-steps), I = 1280 (L2 k-loop remainder)
 ]
 
 
