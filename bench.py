@@ -233,7 +233,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8e4m3",
+        "dtype": "fp8e4m3 in, bf16 MFMA, fp32 acc",
         "data": "synthetic (seeded N(0,1) x, N(0,0.02) weights, softmax top-8 router)",
         "config": {"workload": f"fused fp8 MoE layer E=256 top-8 H=6144 I=2048 T={T}"
                                + (f" zipf({args.zipf})" if args.zipf else " balanced"),
