@@ -332,6 +332,23 @@ def test_full_size_layer(T, zipf):
     _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
 
 
+def test_bf16_output_without_fp32_matches():
+    """The torch mirror writes only the bf16 y unless write_fp32_y is set; the
+    bf16 result is the same bits either way (combine computes one fp32 sum)."""
+    _say("bf16 output with and without fp32 y")
+    E, K, H, I, T = 16, 8, 512, 256, 96
+    c = mc.normal_case(E, K, H, I, T, seed=41, scaled=True)
+    r = mc.run_layer(c)                   # write_fp32_y = True
+    buf = r.buf
+    buf.write_fp32_y = False
+    buf._y_fp32.fill_(12345.0)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    mm.fp8_mega_moe(y, (c.w1, c.s1), (c.w2, c.s2), buf)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.float().cpu().numpy(), r.y)
+    assert bool((buf._y_fp32[:T] == 12345.0).all()), "fp32 y written although not requested"
+
+
 def test_graph_replay_matches_eager():
     """N launches captured in one HIP graph, replayed three times with eager
     work in between; every replay must reproduce the eager output bit for bit
