@@ -105,7 +105,14 @@ def run_layer(c: Case, skip_fetch_l2: bool = False) -> Run:
     y = torch.empty((c.T, c.H), dtype=torch.bfloat16, device="cuda")
     l1 = (c.w1, c.s1) if c.scaled else c.w1
     l2 = (c.w2, c.s2) if c.scaled else c.w2
-    mm.fp8_mega_moe(y, l1, l2, buf)
+    if c.cap:
+        # a slot capacity goes through the C ABI (MegaLaunchArgs::slot_capacity)
+        import ctypes
+        a = buf.make_args(c.T, l1, l2, y_bf16=y, slot_capacity=c.cap)
+        rc = mm.lib().mm_launch_full(ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, f"mm_launch_full status {rc}"
+    else:
+        mm.fp8_mega_moe(y, l1, l2, buf)
     torch.cuda.synchronize()
     offsets = buf.offsets().cpu().numpy()
     slots = int(offsets[-1])

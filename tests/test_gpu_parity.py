@@ -5,6 +5,7 @@ check.cu's staged tolerances; the whole layer at max|d| <= 2e-2 rms(y) and
 cos >= 0.9995.
 """
 import ctypes
+import dataclasses
 import sys
 
 import numpy as np
@@ -327,6 +328,48 @@ def test_full_size_layer(T, zipf):
     for e in {int(order[-1]), int(order[len(order) // 2]), int(order[0])}:
         mc.check_l1(c, r, e, max_rows=48)
         mc.check_l2(c, r, e, max_rows=48)
+    mc.check_reduce(c, r)
+    err, rms, cos = mc.check_e2e_tokens(c, r, [0, 1, T // 2, T - 1])
+    _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
+def test_layer_with_capacity_drops_and_invalid_ids():
+    """Pairs over the slot capacity and pairs with an expert id outside [0, E)
+    get no slot (src/prologue.cuh:150-175) and contribute nothing to y; the
+    rest of the layer runs as usual."""
+    E, K, H, I, T, cap = 32, 8, 1024, 512, 200, 30
+    c = mc.normal_case(E, K, H, I, T, seed=51, scaled=True)
+    idx = c.idx.copy()
+    idx[3, 0], idx[7, 5], idx[100, 2] = -1, E + 3, E
+    c = dataclasses.replace(c, idx=idx, cap=cap)
+    _say(f"layer with cap={cap} and invalid ids")
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    assert int((r.pair_pos < 0).sum()) > 3, "expected capacity drops"
+    for e in range(0, E, 7):
+        mc.check_l1(c, r, e)
+        mc.check_l2(c, r, e)
+    mc.check_reduce(c, r)
+    mc.check_e2e(c, r)
+
+
+def test_full_size_extreme_skew():
+    """T=1024 with every token routed among 16 experts (512 rows each: two
+    256-row items, 16 token tiles) and 240 experts empty."""
+    E, K, H, I, T = 256, 8, 6144, 2048, 1024
+    rng = np.random.default_rng(61)
+    hot = np.sort(rng.choice(E, size=16, replace=False))
+    idx = np.stack([rng.permutation(hot)[:K] for _ in range(T)]).astype(np.int64)
+    wts = rng.random((T, K)).astype(np.float32)
+    wts /= wts.sum(axis=1, keepdims=True)
+    _say("full size extreme skew T=1024 on 16 experts")
+    c = mc.normal_case(E, K, H, I, T, seed=62, scaled=True, idx=idx, wts=wts)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    assert int((r.counts > 0).sum()) == 16
+    for e in hot[:3]:
+        mc.check_l1(c, r, int(e), max_rows=48)
+        mc.check_l2(c, r, int(e), max_rows=48)
     mc.check_reduce(c, r)
     err, rms, cos = mc.check_e2e_tokens(c, r, [0, 1, T // 2, T - 1])
     _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
