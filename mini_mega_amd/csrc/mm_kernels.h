@@ -18,6 +18,9 @@ constexpr int kRouteChunkSmall = 256;
 constexpr int kRouteChunkLarge = 1024;
 constexpr int kRouteSmallP = 8192;
 inline int route_chunk(int P) { return P <= kRouteSmallP ? kRouteChunkSmall : kRouteChunkLarge; }
+// The scan builds the chunk histograms itself (in LDS, no histogram launch)
+// when they fit: nchunks * E <= kFusedHist counters.
+constexpr int kFusedHist = 8192;
 
 constexpr int kGemmThreads = 256;   // 4 waves per workgroup (decode-shaped GEMMs)
 constexpr int kBigThreads = 512;    // 8 waves per workgroup, two per SIMD (large-M GEMMs)
@@ -56,7 +59,8 @@ __global__ void l1_big_kernel(GemmParams p);
 __global__ void l2_big_kernel(GemmParams p);
 
 __global__ void route_hist_kernel(const int64_t*, int, int, int, int*);
-__global__ void route_scan_kernel(int*, int, int, int, int, int, int, int, int*, int*, int*, int*);
+__global__ void route_scan_kernel(const int64_t*, int, int, int*, int, int, int, int, int, int, int,
+                                  int*, int*, int*, int*);
 __global__ void route_scatter_kernel(const int64_t*, int, int, int, int, const int*, const int*,
                                      const int*, uint32_t*, int*);
 __global__ void dispatch_gather_kernel(const uint8_t*, int, int, const uint32_t*, const int*,

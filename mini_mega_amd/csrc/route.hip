@@ -2,8 +2,9 @@
 // the reference's EP dispatch metadata: route_build_body, src/prologue.cuh:
 // 126-226; publish_counts_body :230-256; task_setup_body :269-498).
 //
-// Three stream-ordered kernels over P = tokens * topk (token, k) pairs:
-//   1. route_hist:    per chunk of 1024 pairs, an LDS histogram over experts.
+// Three stream-ordered kernels over P = tokens * topk (token, k) pairs (two
+// for small P, where route_scan builds the histograms itself):
+//   1. route_hist:    per chunk of pairs, an LDS histogram over experts.
 //   2. route_scan:    one workgroup; per expert the exclusive prefix over chunks,
 //                     the capped count, the exclusive prefix over experts
 //                     (slot offsets) and the work-item list (expert, first row).
@@ -63,14 +64,38 @@ __device__ int block_exclusive_scan(int v, int* smem, int* total) {
 }
 
 __global__ void __launch_bounds__(kScanThreads)
-route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int m_tile,
+route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
+                  int* __restrict__ chunk_hist, int nchunks, int E, int cap, int m_tile,
                   int max_items, int nb1, int nb2, int* __restrict__ counts,
                   int* __restrict__ offsets, int* __restrict__ items, int* __restrict__ status) {
     __shared__ int smem[kScanThreads / 64 + 1];
     __shared__ int cut_s[2][8];
+    __shared__ int lh[kFusedHist];   // [chunk][expert] when topk_idx is given
     // the status word of this launch (only this kernel sets its error bits;
     // thread 0 clears it before its own atomicOr below)
     if (threadIdx.x == 0) status[0] = 0;
+    // Small launches (topk_idx given, nchunks * E <= kFusedHist): the chunk
+    // histograms of route_hist_kernel, built here in LDS, 8 pairs' loads in
+    // flight per thread.
+    const bool fused = topk_idx != nullptr;
+    if (fused) {
+        for (int i = threadIdx.x; i < nchunks * E; i += kScanThreads) lh[i] = 0;
+        __syncthreads();
+        for (int p0 = threadIdx.x; p0 < P; p0 += 8 * kScanThreads) {
+            int64_t ev[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = p0 + u * kScanThreads;
+                ev[u] = p < P ? topk_idx[p] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = p0 + u * kScanThreads;
+                if (ev[u] >= 0 && ev[u] < E) atomicAdd(&lh[(p / chunk) * E + (int)ev[u]], 1);
+            }
+        }
+        __syncthreads();
+    }
     // E <= kMaxExperts = kScanThreads: one expert per thread.
     const int e = threadIdx.x;
     int cnt = 0;
@@ -82,7 +107,9 @@ route_scan_kernel(int* __restrict__ chunk_hist, int nchunks, int E, int cap, int
             int h[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                h[u] = c0 + u < nchunks ? chunk_hist[(size_t)(c0 + u) * E + e] : 0;
+                h[u] = c0 + u >= nchunks ? 0
+                       : fused           ? lh[(c0 + u) * E + e]
+                                         : chunk_hist[(size_t)(c0 + u) * E + e];
 #pragma unroll
             for (int u = 0; u < 8; ++u)
                 if (c0 + u < nchunks) {
