@@ -353,6 +353,52 @@ def test_layer_with_capacity_drops_and_invalid_ids():
     mc.check_e2e(c, r)
 
 
+def _sweep_case(seed):
+    """A random small layer: shape, top-k, token count, scales, routing skew,
+    expert window and slot capacity drawn from one seed."""
+    rng = np.random.default_rng(1000 + seed)
+    E = int(rng.choice([4, 8, 16, 32, 64, 128]))
+    K = int(rng.integers(1, min(8, E) + 1))
+    H = int(rng.choice([256, 512, 768, 1024]))
+    I = int(rng.choice([128, 256, 512, 768]))
+    T = int(rng.integers(1, 401))
+    scaled = bool(rng.integers(0, 2))
+    zipf = 1.1 if rng.random() < 0.4 else None
+    win = int(rng.choice([0, 0, 16, 32, 64, 128, 256]))
+    c = mc.normal_case(E, K, H, I, T, seed=300 + seed, scaled=scaled, zipf=zipf, win=win)
+    if rng.random() < 0.3:
+        # between one and two times the mean expert load: busy experts drop
+        # pairs, but most tokens keep some (a cap that zeroes most rows makes
+        # rms(y) small against the surviving rows, and the bf16 half-ulp of
+        # those alone passes 2e-2 rms; test_layer_with_capacity_drops_and_
+        # invalid_ids covers heavy drops)
+        mean = -(-T * K // E)
+        c = dataclasses.replace(c, cap=int(rng.integers(mean, 2 * mean + 1)))
+    return c, zipf
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_sweep(seed):
+    """Random small layers (seeded): routing bit-exact, L1 / L2 on the busiest
+    and one other active expert at the staged tolerances, REDUCE, and the
+    whole layer at the end-to-end bar."""
+    c, zipf = _sweep_case(seed)
+    _say(f"sweep seed={seed}: E={c.E} K={c.K} H={c.H} I={c.I} T={c.T} scaled={c.scaled} "
+         f"zipf={zipf} win={c.win} cap={c.cap}")
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    active = np.flatnonzero(r.counts > 0)
+    if active.size:
+        busiest = int(np.argmax(r.counts))
+        other = int(active[np.random.default_rng(seed).integers(0, active.size)])
+        for e in sorted({busiest, other}):
+            mc.check_l1(c, r, e)
+            mc.check_l2(c, r, e)
+    mc.check_reduce(c, r)
+    err, rms, cos = mc.check_e2e(c, r)
+    _say(f"  e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
 def test_full_size_extreme_skew():
     """T=1024 with every token routed among 16 experts (512 rows each: two
     256-row items, 16 token tiles) and 240 experts empty."""
