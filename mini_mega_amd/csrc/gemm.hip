@@ -44,15 +44,15 @@ struct Stage {
 };
 
 template <int MT>
-__device__ __forceinline__ void load_stage(Stage<MT>& s, const uint8_t* const* wt,
+__device__ __forceinline__ void load_stage(Stage<MT>& s, const WTiles<4>& wt,
                                            const uint8_t* const* xr, int kt,
                                            const uint8_t* wsf0, const uint8_t* wsf1,
                                            const uint8_t* const* xsf) {
-    const size_t wo = (size_t)kt * kTileBytes;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        s.a[t][0] = load16_stream(wt[t] + wo);
-        s.a[t][1] = load16_stream(wt[t] + wo + 1024);
+        const uint8_t* a = wt.at(t, kt);
+        s.a[t][0] = load16_stream(a);
+        s.a[t][1] = load16_stream(a + 1024);
     }
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
@@ -95,7 +95,7 @@ struct MmaBf16 {
 
 // K loop with an S-stage register pipeline over KT k-steps of 128.
 template <class Mma, int MT, int S>
-__device__ __forceinline__ void gemm_mainloop(v4f (&acc)[4][MT], const uint8_t* const* wt,
+__device__ __forceinline__ void gemm_mainloop(v4f (&acc)[4][MT], const WTiles<4>& wt,
                                               const uint8_t* const* xr, int KT,
                                               const uint8_t* wsf0, const uint8_t* wsf1,
                                               const uint8_t* const* xsf, int ntiles) {
@@ -135,12 +135,12 @@ __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
     const int rho = (h0 / G) * 2 * G + (h0 % G);
     const int ntg = rho >> 4, ntu = ntg + (G >> 4);
     const uint8_t* we = p.w + (size_t)e * (size_t)(2 * I) * H;
-    const size_t tstride = (size_t)KT * kTileBytes;
-    const uint8_t* wt[4];
-    wt[0] = we + (size_t)ntg * tstride + lane * 16;
-    wt[1] = wt[0] + tstride;
-    wt[2] = we + (size_t)ntu * tstride + lane * 16;
-    wt[3] = wt[2] + tstride;
+    WTiles<4> wt;
+    wt.KT = KT;
+    wt.set(0, we, ntg, lane);
+    wt.set(1, we, ntg + 1, lane);
+    wt.set(2, we, ntu, lane);
+    wt.set(3, we, ntu + 1, lane);
     const uint8_t* wsf0 = nullptr;
     const uint8_t* wsf1 = nullptr;
     if (p.w_sf) {
@@ -250,10 +250,10 @@ __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
     const int n0 = blockIdx.x * kL2BlockN + wave * 64;
     const int nt0 = n0 >> 4;
     const uint8_t* we = p.w + (size_t)e * (size_t)H * I;
-    const size_t tstride = (size_t)KT * kTileBytes;
-    const uint8_t* wt[4];
+    WTiles<4> wt;
+    wt.KT = KT;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) wt[t] = we + (size_t)(nt0 + t) * tstride + lane * 16;
+    for (int t = 0; t < 4; ++t) wt.set(t, we, nt0 + t, lane);
     const uint8_t* wsf = p.w_sf ? p.w_sf + ((size_t)e * (H / 128) + (n0 >> 7)) * KT : nullptr;
 
     const uint8_t* xr[MT];

@@ -61,14 +61,14 @@ struct alignas(16) BigSmem {
 // When NT*128 is not a multiple of T some threads redo another thread's
 // chunk (same bytes to the same LDS slot), which keeps every thread's work
 // uniform.  XS register stages: with two, the rows of k-step kt+2 are in
-// flight while kt+1 is written to LDS; with one (where registers go to
-// accumulators, and a k-step's MFMAs alone cover an L2 hit), kt+1 is loaded
-// during kt.
+// flight while kt+1 is written to LDS; with one (above 12 token tiles, where
+// registers go to accumulators, and a k-step's 4*NT MFMA groups alone cover
+// an L2 hit; measured even with two at T = 8192), kt+1 is loaded during kt.
 template <int W, int NT>
 struct XLoader {
     static constexpr int kThreads = Geo<W>::kThreads;
     static constexpr int U = (NT * 128 + kThreads - 1) / kThreads;
-    static constexpr int XS = (W == 8 || NT <= 8) ? 2 : 1;
+    static constexpr int XS = NT <= 12 ? 2 : 1;
     const uint8_t* base;
     uint32_t off[U];
     v4i reg[XS][U];
@@ -107,12 +107,12 @@ struct WStage {
 };
 
 template <int WT>
-__device__ __forceinline__ void w_load(WStage<WT>& w, const uint8_t* const* wt, int kt) {
-    const size_t o = (size_t)kt * kTileBytes;
+__device__ __forceinline__ void w_load(WStage<WT>& w, const WTiles<WT>& wt, int kt) {
 #pragma unroll
     for (int t = 0; t < WT; ++t) {
-        w.a[t][0] = load16_stream(wt[t] + o);
-        w.a[t][1] = load16_stream(wt[t] + o + 1024);
+        const uint8_t* a = wt.at(t, kt);
+        w.a[t][0] = load16_stream(a);
+        w.a[t][1] = load16_stream(a + 1024);
     }
 }
 
@@ -169,7 +169,7 @@ constexpr int big_read_ahead() { return (W == 8 && NT > 12) ? 2 : 3; }
 template <int W, int NT, int S, int s>
 __device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                          XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
-                                         const uint8_t* const* wt, v8bf (&a0)[Geo<W>::kWT],
+                                         const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
                                          int kt, int KT) {
     constexpr int kWT = Geo<W>::kWT;
     constexpr int XS = XLoader<W, NT>::XS, U = XLoader<W, NT>::U;
@@ -241,7 +241,7 @@ __device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& s
 template <int W, int NT, int S, int s>
 __device__ __forceinline__ void big_group(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                           XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
-                                          const uint8_t* const* wt, v8bf (&a0)[Geo<W>::kWT],
+                                          const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
                                           int kb, int KT) {
     big_step<W, NT, S, s>(acc, sm, xl, w, wt, a0, kb + s, KT);
     if constexpr (s + 1 < S) big_group<W, NT, S, s + 1>(acc, sm, xl, w, wt, a0, kb, KT);
@@ -251,7 +251,7 @@ __device__ __forceinline__ void big_group(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& 
 template <int W, int NT, int S, int r>
 __device__ __forceinline__ void big_tail(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                          XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
-                                         const uint8_t* const* wt, v8bf (&a0)[Geo<W>::kWT],
+                                         const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
                                          int KF, int KT) {
     if (KF + r < KT) {
         big_step<W, NT, S, r>(acc, sm, xl, w, wt, a0, KF + r, KT);
@@ -265,7 +265,7 @@ __device__ __forceinline__ void big_tail(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& s
 // KT is not a multiple of S) runs through the guarded tail.
 template <int W, int NT, int S>
 __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
-                                             XLoader<W, NT>& xl, const uint8_t* const* wt,
+                                             XLoader<W, NT>& xl, const WTiles<Geo<W>::kWT>& wt,
                                              int KT) {
     constexpr int kWT = Geo<W>::kWT;
     constexpr int XS = XLoader<W, NT>::XS;
@@ -408,11 +408,10 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
         return (p.perm[slot] / (uint32_t)p.topk) * (uint32_t)H;
     });
     const uint8_t* we = p.w + (size_t)it.e * (size_t)(2 * I) * H;
-    const size_t tstride = (size_t)KT * kTileBytes;
-    const uint8_t* wt[kWT];
+    WTiles<kWT> wt;
+    wt.KT = KT;
 #pragma unroll
-    for (int t = 0; t < kWT; ++t)
-        wt[t] = we + (size_t)(l1_tile_row<W>(it.bx, kWT * wave + t, G) >> 4) * tstride + lane * 16;
+    for (int t = 0; t < kWT; ++t) wt.set(t, we, l1_tile_row<W>(it.bx, kWT * wave + t, G) >> 4, lane);
     v4f acc[kWT][NT];
     big_mainloop<W, NT, big_stages<W, NT, false>()>(acc, sm, xl, wt, KT);
 
@@ -518,10 +517,10 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     });
     const int n0 = it.bx * kL2BlockN + wave * (kL2BlockN / W);   // the wave's output channels
     const uint8_t* we = p.w + (size_t)it.e * (size_t)H * I;
-    const size_t tstride = (size_t)KT * kTileBytes;
-    const uint8_t* wt[kWT];
+    WTiles<kWT> wt;
+    wt.KT = KT;
 #pragma unroll
-    for (int t = 0; t < kWT; ++t) wt[t] = we + (size_t)((n0 >> 4) + t) * tstride + lane * 16;
+    for (int t = 0; t < kWT; ++t) wt.set(t, we, (n0 >> 4) + t, lane);
     v4f acc[kWT][NT];
     big_mainloop<W, NT, big_stages<W, NT, true>()>(acc, sm, xl, wt, KT);
 #pragma unroll

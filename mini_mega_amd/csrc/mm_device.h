@@ -33,6 +33,25 @@ __host__ __device__ inline size_t tile_byte(int r, int k, int k_cols) {
            (size_t)(((kk & 31) >> 4) * 1024 + (rr + 16 * (kk >> 5)) * 16 + (kk & 15));
 }
 
+// A wave's weight tiles: each tile row's start, wave-uniform (a scalar
+// register pair: the k-step offset arithmetic runs on the scalar unit, and
+// a load is a scalar base plus the lane's 16-byte offset); at(t, kt) is the
+// lane's 16 bytes of tile t's k-step kt.
+template <int WT>
+struct WTiles {
+    const uint8_t* row[WT];
+    int KT;
+    uint32_t lane16;
+    __device__ __forceinline__ void set(int t, const uint8_t* mat, int nt, int lane) {
+        nt = __builtin_amdgcn_readfirstlane(nt);
+        row[t] = mat + (size_t)nt * (size_t)KT * kTileBytes;
+        lane16 = (uint32_t)lane * 16u;
+    }
+    __device__ __forceinline__ const uint8_t* at(int t, int kt) const {
+        return row[t] + (size_t)kt * kTileBytes + lane16;
+    }
+};
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
