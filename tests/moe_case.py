@@ -94,8 +94,11 @@ class Run:
     status: np.ndarray
 
 
-def run_layer(c: Case, skip_fetch_l2: bool = False) -> Run:
-    buf = mm.get_symm_buffer_for_mega_moe(None, c.E, c.T, c.K, c.H, c.I, expert_window=c.win)
+def run_layer(c: Case, skip_fetch_l2: bool = False, buf=None) -> Run:
+    """One launch of the layer on case c (in `buf` when given: a workspace
+    reused across launches)."""
+    if buf is None:
+        buf = mm.get_symm_buffer_for_mega_moe(None, c.E, c.T, c.K, c.H, c.I, expert_window=c.win)
     buf.write_fp32_y = True
     buf.x.view(torch.uint8)[:c.T].copy_(torch.from_numpy(c.x))
     if c.xsf is not None:

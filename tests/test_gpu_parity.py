@@ -438,6 +438,24 @@ def test_bf16_output_without_fp32_matches():
     assert bool((buf._y_fp32[:T] == 12345.0).all()), "fp32 y written although not requested"
 
 
+def test_workspace_reuse_across_sizes():
+    """One workspace, launches of 300, 37 and 300 tokens with different
+    routings and weights: nothing of a larger earlier launch (work items, XCD
+    unit ranges, chunk histograms) may leak into a smaller later one.  With
+    1024 experts the routing alternates between the separate histogram launch
+    (300 tokens: 10 chunks x 1024 counters) and the scan's own (37 tokens)."""
+    E, K, H, I = 1024, 8, 256, 128
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, 300, K, H, I)
+    for T, seed in ((300, 71), (37, 72), (300, 73)):
+        _say(f"workspace reuse T={T} seed={seed}")
+        c = mc.normal_case(E, K, H, I, T, seed=seed, scaled=True)
+        r = mc.run_layer(c, buf=buf)
+        mc.check_routing(c, r)
+        mc.check_reduce(c, r)
+        err, rms, cos = mc.check_e2e(c, r)
+        _say(f"  e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
 def test_graph_replay_matches_eager():
     """N launches captured in one HIP graph, replayed three times with eager
     work in between; every replay must reproduce the eager output bit for bit
