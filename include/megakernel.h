@@ -97,7 +97,8 @@ struct MegaLaunchArgs {
     const uint8_t* x_sf = nullptr;         // [tokens][H/128] UE8M0 bytes, null = 2^0
     const uint8_t* w1_sf = nullptr;        // [E][2I/128][H/128] UE8M0, null = 2^0
     const uint8_t* w2_sf = nullptr;        // [E][H/128][I/128]  UE8M0, null = 2^0
-    int ffn_ue8m0 = 0;                     // L1 output requant: per-128 UE8M0 (1) or raw (0)
+    int ffn_ue8m0 = 0;                     // L1 output requant: per-128 UE8M0 (1) or raw (0);
+                                           // must be 1 exactly when scales are given
     uint16_t* y_bf16 = nullptr;            // [tokens][H] bf16 (may be null if y)
 };
 

@@ -67,6 +67,11 @@ int bind(const MegaLaunchArgs& a, Bound& b, bool need_weights) {
     const bool any_sf = a.x_sf || a.w1_sf || a.w2_sf;
     if (any_sf && !(a.w1_sf && a.w2_sf)) return kErrNullPointer;
     if (any_sf && !a.in_bf16 && !a.x_sf) return kErrNullPointer;
+    // the L1 output's quantisation follows the scale mode, as in the reference
+    // (per-128 UE8M0 with block-scaled operands, torch/mxmegakernel/utils/
+    // math.py:13-72; the saturating e4m3 cast without, src/bench_check.cuh:
+    // 362-380); a mixed mode is no reference path
+    if ((a.ffn_ue8m0 != 0) != any_sf) return kErrUnsupported;
     b.L = layout(a.max_tokens, a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
     if (a.workspace_bytes < b.L.total) return kErrWorkspace;
     b.ws = reinterpret_cast<uint8_t*>(a.rwk);

@@ -72,6 +72,13 @@ def test_launch_rejects_null_workspace_without_touching_gpu():
     a = mm.MegaLaunchArgs(tokens=4, max_tokens=4, rwk=1, self=1, topk_idx=1, w1=1, w2=1,
                           workspace_bytes=16)
     assert L.mm_launch_full(ctypes.byref(a), None) == 3  # kErrWorkspace
+    # the L1 output's quantisation must follow the scale mode
+    a = mm.MegaLaunchArgs(tokens=4, max_tokens=4, rwk=1, self=1, topk_idx=1, w1=1, w2=1,
+                          ffn_ue8m0=1)
+    assert L.mm_launch_full(ctypes.byref(a), None) == 6  # kErrUnsupported
+    a = mm.MegaLaunchArgs(tokens=4, max_tokens=4, rwk=1, self=1, topk_idx=1, w1=1, w2=1,
+                          x_sf=1, w1_sf=1, w2_sf=1, ffn_ue8m0=0)
+    assert L.mm_launch_full(ctypes.byref(a), None) == 6  # kErrUnsupported
 
 
 def _pack_numpy(w):
