@@ -333,6 +333,27 @@ def test_full_size_layer(T, zipf):
     _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
 
 
+@pytest.mark.parametrize("win", [16, 32])
+def test_full_size_decode_windows(win):
+    """T=512 at full size through the decode-shaped kernels (windows of 16 /
+    32 rows, the reference's small-window tasks): routing exact, staged L1/L2
+    on the busiest and the lightest expert, REDUCE, the chain on a subset."""
+    T = 512
+    _say(f"full size T={T} win={win}")
+    c = mc.normal_case(256, 8, 6144, 2048, T, seed=81, scaled=True, win=win)
+    r = mc.run_layer(c)
+    assert int(r.buf.layout.m_tile) == win
+    mc.check_routing(c, r)
+    nz = np.nonzero(r.counts)[0]
+    order = nz[np.argsort(r.counts[nz], kind="stable")]
+    for e in {int(order[-1]), int(order[0])}:
+        mc.check_l1(c, r, e, max_rows=48)
+        mc.check_l2(c, r, e, max_rows=48)
+    mc.check_reduce(c, r)
+    err, rms, cos = mc.check_e2e_tokens(c, r, [0, T // 3, T - 1])
+    _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
 def test_layer_with_capacity_drops_and_invalid_ids():
     """Pairs over the slot capacity and pairs with an expert id outside [0, E)
     get no slot (src/prologue.cuh:150-175) and contribute nothing to y; the
