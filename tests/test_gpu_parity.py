@@ -296,6 +296,41 @@ def test_layer_bf16_input_fold():
     mc.check_e2e(c, r)
 
 
+def test_single_token_then_empty_batch():
+    """T=1 (K experts of one row each) at the staged and e2e tolerances; then
+    T=0 on the same buffer: the launch succeeds, the expert counts are
+    rewritten to zero (no stale counts from the previous call) and the
+    cumulative per-expert stats gain nothing (reference
+    mega/__init__.py:610-655 with num_tokens = 0)."""
+    E, K, H, I = 32, 8, 1024, 512
+    _say("single token T=1")
+    c = mc.normal_case(E, K, H, I, 1, seed=43, scaled=True)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    for e in np.flatnonzero(r.counts):
+        mc.check_l1(c, r, int(e))
+        mc.check_l2(c, r, int(e))
+    mc.check_reduce(c, r)
+    mc.check_e2e(c, r)
+
+    _say("empty batch T=0 after a T=1 call")
+    buf = r.buf
+    stats = torch.zeros(E, dtype=torch.int64, device="cuda")
+    y1 = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
+    mm.fp8_mega_moe(y1, (c.w1, c.s1), (c.w2, c.s2), buf,
+                    cumulative_local_expert_recv_stats=stats)
+    torch.cuda.synchronize()
+    assert int(stats.sum()) == K and int(buf.counts().sum()) == K
+    assert np.array_equal(y1.float().cpu().numpy(), r.y)
+    y0 = torch.empty((0, H), dtype=torch.bfloat16, device="cuda")
+    mm.fp8_mega_moe(y0, (c.w1, c.s1), (c.w2, c.s2), buf,
+                    cumulative_local_expert_recv_stats=stats)
+    torch.cuda.synchronize()
+    assert int(buf.counts().abs().sum()) == 0
+    assert int(buf.offsets().abs().sum()) == 0
+    assert int(stats.sum()) == K
+
+
 # -------------------------------------------------- check.cu-identical inputs --
 def test_checkcu_inputs_full_size_t512():
     """check.cu's own inputs at R=32, TPR=16 (T=512) remapped to one GPU:
