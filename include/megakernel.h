@@ -92,7 +92,9 @@ struct MegaLaunchArgs {
     int topk = 8;
     int hidden = 6144;                     // H
     int intermediate = 2048;               // I
-    int max_tokens = 0;                    // tokens the workspace was laid out for
+    int max_tokens = 0;                    // tokens the workspace was laid out for; with
+                                           // topk, H, I: max_tokens*H <= 2^32 and
+                                           // max_tokens*topk*I <= 2^32 (kErrBadDims)
     int64_t workspace_bytes = 0;           // size of *rwk
     const uint8_t* x_sf = nullptr;         // [tokens][H/128] UE8M0 bytes, null = 2^0
     const uint8_t* w1_sf = nullptr;        // [E][2I/128][H/128] UE8M0, null = 2^0
@@ -198,7 +200,8 @@ int mm_abi_version(void);
 size_t mm_args_size(void);
 // Offset of a MegaLaunchArgs field by name, or -1 if unknown.
 long long mm_args_offset(const char* field);
-// Writes layout(...) into *out; returns status.
+// Writes layout(...) into *out; returns status (kErrBadDims for unsupported
+// dims or a capacity past the 32-bit activation row offsets, see max_tokens).
 int mm_layout(int max_tokens, int topk, int num_experts, int hidden,
               int intermediate, int win_cap, fp8mega::MegaLayout* out);
 int mm_launch_prelude(const fp8mega::MegaLaunchArgs* a, void* stream);

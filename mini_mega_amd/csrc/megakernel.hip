@@ -47,6 +47,18 @@ int check_dims(int topk, int E, int H, int I, int win_cap) {
     return kOk;
 }
 
+// The GEMMs' activation loaders address a row as a 32-bit byte offset
+// (token * H into x for L1, slot * I into the intermediate for L2), and slots
+// are int: capacities past those ranges are rejected rather than wrapped.
+int check_capacity(int64_t max_tokens, int topk, int H, int I) {
+    if (max_tokens <= 0) return kErrBadDims;
+    const int64_t pairs = max_tokens * topk;
+    if (pairs > INT32_MAX || max_tokens * H > (int64_t(1) << 32) ||
+        pairs * I > (int64_t(1) << 32))
+        return kErrBadDims;
+    return kOk;
+}
+
 struct Bound {
     const uint8_t* x = nullptr;
     const uint8_t* x_sf = nullptr;
@@ -61,7 +73,9 @@ int bind(const MegaLaunchArgs& a, Bound& b, bool need_weights) {
     if (st != kOk) return st;
     if (a.rwk == nullptr || a.topk_idx == nullptr || a.self == nullptr) return kErrNullPointer;
     if (need_weights && (a.w1 == nullptr || a.w2 == nullptr)) return kErrNullPointer;
-    if (a.tokens < 0 || a.max_tokens <= 0) return kErrBadDims;
+    if (a.tokens < 0) return kErrBadDims;
+    st = check_capacity(a.max_tokens, a.topk, a.hidden, a.intermediate);
+    if (st != kOk) return st;
     if (a.tokens > a.max_tokens) return kErrTooManyTokens;
     if (a.R != 1 || a.rank != 0) return kErrUnsupported;
     const bool any_sf = a.x_sf || a.w1_sf || a.w2_sf;
@@ -414,7 +428,8 @@ int mm_layout(int max_tokens, int topk, int num_experts, int hidden, int interme
     if (!out) return fp8mega::kErrNullPointer;
     const int st = fp8mega::check_dims(topk, num_experts, hidden, intermediate, win_cap);
     if (st != fp8mega::kOk) return st;
-    if (max_tokens <= 0) return fp8mega::kErrBadDims;
+    const int cst = fp8mega::check_capacity(max_tokens, topk, hidden, intermediate);
+    if (cst != fp8mega::kOk) return cst;
     *out = fp8mega::layout(max_tokens, topk, num_experts, hidden, intermediate, win_cap);
     return fp8mega::kOk;
 }

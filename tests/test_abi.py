@@ -57,10 +57,22 @@ def test_layout_regions_aligned_and_disjoint(T):
 
 @pytest.mark.parametrize("dims", [(32, 8, 256, 100, 2048), (32, 8, 256, 6144, 200),
                                   (32, 0, 256, 6144, 2048), (32, 8, 2000, 6144, 2048),
-                                  (0, 8, 256, 6144, 2048)])
+                                  (0, 8, 256, 6144, 2048),
+                                  # past the 32-bit activation row offsets: T*K*I > 2^32,
+                                  # T*H > 2^32
+                                  (262145, 8, 256, 6144, 2048), (699051, 1, 256, 6144, 128)])
 def test_layout_rejects_bad_dims(dims):
     with pytest.raises(mm.MegaError):
         mm.layout(*dims)
+
+
+def test_capacity_limit_is_inclusive():
+    """T*K*I = 2^32 exactly (the last row's offsets still fit) is laid out;
+    one token more is rejected by the layout and by a launch alike."""
+    L = mm.layout(262144, 8, 256, 6144, 2048)
+    assert L.max_pairs == 262144 * 8
+    a = mm.MegaLaunchArgs(tokens=4, max_tokens=262145, rwk=1, self=1, topk_idx=1, w1=1, w2=1)
+    assert mm.lib().mm_launch_full(ctypes.byref(a), None) == 2  # kErrBadDims
 
 
 def test_launch_rejects_null_workspace_without_touching_gpu():
