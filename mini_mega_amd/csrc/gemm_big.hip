@@ -110,9 +110,9 @@ template <int WT>
 __device__ __forceinline__ void w_load(WStage<WT>& w, const WTiles<WT>& wt, int kt) {
 #pragma unroll
     for (int t = 0; t < WT; ++t) {
-        const uint8_t* a = wt.at(t, kt);
-        w.a[t][0] = load16_stream(a);
-        w.a[t][1] = load16_stream(a + 1024);
+        const int o = kt * kTileBytes + (int)wt.lane16;
+        w.a[t][0] = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o);
+        w.a[t][1] = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o + 1024);
     }
 }
 

@@ -128,6 +128,22 @@ __device__ __forceinline__ v4i load16_stream(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
 }
 
+constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer resource word 3: 32-bit data format
+constexpr int kBufferNT = 2;               // buffer load cache policy bit: nt (non-temporal)
+
+// The same non-temporal 16-byte weight load through a buffer resource over one
+// tile row (base and length in scalar registers, the byte offset `off` in a
+// vector register; offsets past row_bytes read zeros).  The LDS-staged GEMMs
+// use it: measured on MI355X against the global-address form, L2 536-539 vs
+// 546-547 us at T = 512 and 645-657 vs 658-666 us at T = 2048, L1 within
+// +-5 us, layer at T = 8192 5061 vs 5105 us; the sc0 / sc1 scope bits on top
+// of nt changed nothing.
+__device__ __forceinline__ v4i load16_row_stream(const uint8_t* row, int row_bytes, int off) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(row), (short)0, row_bytes, kBufferWord3);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufferNT);
+}
+
 __device__ __forceinline__ v4i load16(const uint8_t* p) {
     return *reinterpret_cast<const v4i*>(p);
 }
