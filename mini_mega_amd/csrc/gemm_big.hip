@@ -85,7 +85,7 @@ struct XLoader {
 
     __device__ __forceinline__ void issue(int kt, int rs) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) reg[rs][u] = load16(base + off[u] + kt * kTileK);
+        for (int u = 0; u < U; ++u) reg[rs][u] = load16_rows(base, off[u], kt * kTileK);
     }
     // Writes chunk u of register stage rs, scaled by 2^(e - 127), to LDS stage xw.
     __device__ __forceinline__ void commit_chunk(uint8_t* xw, int rs, int u, uint32_t e) {
@@ -110,9 +110,9 @@ template <int WT>
 __device__ __forceinline__ void w_load(WStage<WT>& w, const WTiles<WT>& wt, int kt) {
 #pragma unroll
     for (int t = 0; t < WT; ++t) {
-        const int o = kt * kTileBytes + (int)wt.lane16;
-        w.a[t][0] = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o);
-        w.a[t][1] = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o + 1024);
+        const int o = (int)wt.lane16, so = kt * kTileBytes;
+        w.a[t][0] = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o, so);
+        w.a[t][1] = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o + 1024, so);
     }
 }
 

@@ -132,16 +132,31 @@ constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer resource word 3: 32-bi
 constexpr int kBufferNT = 2;               // buffer load cache policy bit: nt (non-temporal)
 
 // The same non-temporal 16-byte weight load through a buffer resource over one
-// tile row (base and length in scalar registers, the byte offset `off` in a
-// vector register; offsets past row_bytes read zeros).  The LDS-staged GEMMs
-// use it: measured on MI355X against the global-address form, L2 536-539 vs
-// 546-547 us at T = 512 and 645-657 vs 658-666 us at T = 2048, L1 within
-// +-5 us, layer at T = 8192 5061 vs 5105 us; the sc0 / sc1 scope bits on top
-// of nt changed nothing.
-__device__ __forceinline__ v4i load16_row_stream(const uint8_t* row, int row_bytes, int off) {
+// tile row: base and length in scalar registers, the lane's byte offset `off`
+// in a vector register (loop-invariant), the k-step's `soff` in a scalar one,
+// so the k-loop spends no vector adds on addresses; lane offsets past
+// row_bytes read zeros.  The LDS-staged GEMMs use it: measured on MI355X
+// against the global-address form, L2 536-539 vs 546-547 us at T = 512 and
+// 645-657 vs 658-666 us at T = 2048, L1 within +-5 us, layer at T = 8192 5061
+// vs 5105 us.  With the k-step in soff (and the activation loads below) the
+// layer at T = 8192 took 5107-5119 vs 5150-5162 us on one box and 5014 vs
+// 5033 us on another, Zipf(1.1) T = 2048 1951 vs 1964 us, T = 512 and
+// T = 2048 even.  The sc0 / sc1 scope bits on top of nt changed nothing.
+__device__ __forceinline__ v4i load16_row_stream(const uint8_t* row, int row_bytes, int off,
+                                                 int soff) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(row), (short)0, row_bytes, kBufferWord3);
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufferNT);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, kBufferNT);
+}
+
+// Cached 16-byte load at base + off + soff through a buffer resource over the
+// whole 32-bit range from `base` (wave-uniform): the per-lane row offset in a
+// vector register, the k-step in a scalar one.  The callers' offsets stay
+// below 2^32 by the capacity limit the host enforces.
+__device__ __forceinline__ v4i load16_rows(const uint8_t* base, uint32_t off, int soff) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(base), (short)0, -1, kBufferWord3);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, 0);
 }
 
 __device__ __forceinline__ v4i load16(const uint8_t* p) {
