@@ -50,6 +50,23 @@ enum MegaStatus : int {
     kErrTooManyTokens = 4,  // tokens > max_tokens the workspace was laid out for
     kErrLaunch = 5,         // hipLaunchKernel failed
     kErrUnsupported = 6,    // option not supported by this build
+    kErrDevice = 7,         // read_status: the device status word reports an error
+};
+
+// Device status words: the workspace region MegaLayout::status, rewritten by
+// the routing of every launch (launch_prelude / launch_compute / launch_full
+// without skip_prologue) and readable after it with read_status():
+//   [0]  error bits (kStatusItemOverflow: the work-item table overflowed; the
+//        GEMMs then skip the experts past it -- the layout's bound makes this
+//        unreachable, the bit guards the kernels' assumption)
+//   [1]  work items, [2] routed slots,
+//   [3]  pairs dropped by slot_capacity,
+//   [4]  pairs whose expert id is outside [0, num_experts) (dropped)
+//   [16..24], [32..40] the big GEMMs' XCD unit ranges (L1, L2)
+// The reference returns no status (src/megakernel.h:117-130): its launches
+// are void and its host CHECKs exit (src/host_layout.cuh:18-26).
+enum MegaDeviceStatus : int {
+    kStatusItemOverflow = 1,
 };
 
 // One launch's host arguments (reference: src/megakernel.h:54-114; fields
@@ -159,6 +176,13 @@ void fill_weights_lane(uint8_t* w, int n_rows, int k_cols, uint32_t seed,
 void dump_kernel_resources();
 // Status of the last call made by this host thread (kOk when it succeeded).
 int last_error();
+// Copies the first n (1..64) device status words of the workspace a.rwk into
+// host memory `out` once the work queued on `stream` has finished: it
+// synchronises `stream`, so it is not for use under graph capture.  Returns
+// kOk, kErrDevice when out[0] (the error bits) is non-zero, or an argument
+// error (no reference counterpart; the single-GPU form of the device error
+// word a caller reads after sync).
+int read_status(const MegaLaunchArgs& a, int32_t* out, int n, hipStream_t stream);
 
 // ---- layout / data-preparation helpers (no reference counterpart in the
 // ---- C++ header; the reference does these in torch/mxmegakernel/mega/__init__.py)
@@ -212,6 +236,8 @@ int mm_launch_reduce(const fp8mega::MegaLaunchArgs* a, void* stream);
 int mm_launch_full(const fp8mega::MegaLaunchArgs* a, void* stream);
 int mm_launch_empty(int grid, int threads, long long smem, void* stream);
 int mm_launch_dispatch(const fp8mega::MegaLaunchArgs* a, uint8_t* pool, void* stream);
+// fp8mega::read_status (synchronises `stream`).
+int mm_read_status(const fp8mega::MegaLaunchArgs* a, int* out, int n, void* stream);
 int mm_fill_weights_lane(uint8_t* w, int n_rows, int k_cols, unsigned seed,
                          void* stream);
 int mm_pack_weights(uint8_t* dst, const uint8_t* src, int n_mats, int n_rows,
@@ -228,4 +254,19 @@ int mm_quant_act(const uint16_t* x_bf16, int rows, int cols, uint8_t* q,
 int mm_selftest_convert(const float* in, int n, uint8_t* out8, uint16_t* out16,
                         void* stream);
 void mm_dump_kernel_resources(void);
+
+// ---- measurement probes (no reference counterpart; nothing on the layer's
+// ---- path calls them; they back the numeric design and the measured peaks)
+// out[r][n] = sum_k a[r][k] * b[n][k] for 16 rows, fp8 e4m3 operands
+// ([16][K] and [N][K] row-major, K % 128 == 0, N % 16 == 0): mode 0 on the
+// 16x16x128 fp8 MFMA, mode 1 on the bf16 MFMA after the exact conversion.
+int mm_probe_mfma_dot(const uint8_t* a, const uint8_t* b, int K, int N, int mode, float* out,
+                      void* stream);
+// Reads `bytes` (a multiple of 16) once with non-temporal 16-byte loads;
+// sink holds grid * 256 words.
+int mm_probe_stream_read(const uint8_t* src, unsigned long long bytes, uint32_t* sink,
+                         int grid, void* stream);
+// grid workgroups of 4 waves, each running iters x 8 independent MFMAs
+// (mode 0: 16x16x32 bf16, mode 1: 16x16x128 fp8); sink holds grid * 4 floats.
+int mm_probe_mfma_rate(int mode, int iters, int grid, float* sink, void* stream);
 }

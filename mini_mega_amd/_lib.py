@@ -49,7 +49,9 @@ class MegaLayout(ctypes.Structure):
 STATUS_NAMES = {
     0: "ok", 1: "null pointer", 2: "unsupported dims", 3: "workspace too small",
     4: "tokens exceed max_tokens", 5: "kernel launch failed", 6: "unsupported option",
+    7: "device status word reports an error",
 }
+ERR_DEVICE = 7
 
 
 class MegaError(RuntimeError):
@@ -61,9 +63,10 @@ class MegaError(RuntimeError):
 EXPORTS = (
     "mm_abi_version", "mm_args_size", "mm_args_offset", "mm_layout", "mm_launch_prelude",
     "mm_launch_compute", "mm_launch_l1", "mm_launch_l2", "mm_launch_reduce", "mm_launch_full",
-    "mm_launch_empty", "mm_launch_dispatch", "mm_fill_weights_lane", "mm_pack_weights",
+    "mm_launch_empty", "mm_launch_dispatch", "mm_read_status", "mm_fill_weights_lane", "mm_pack_weights",
     "mm_pack_weights_from_reference",
     "mm_fill_weights_normal", "mm_quant_act", "mm_selftest_convert", "mm_dump_kernel_resources",
+    "mm_probe_mfma_dot", "mm_probe_stream_read", "mm_probe_mfma_rate",
 )
 
 _lib = None
@@ -92,6 +95,8 @@ def lib():
         getattr(L, n).argtypes = [A, c_vp]
     L.mm_launch_dispatch.restype = c_int
     L.mm_launch_dispatch.argtypes = [A, c_vp, c_vp]
+    L.mm_read_status.restype = c_int
+    L.mm_read_status.argtypes = [A, c_vp, c_int, c_vp]
     L.mm_launch_empty.restype = c_int
     L.mm_launch_empty.argtypes = [c_int, c_int, ctypes.c_longlong, c_vp]
     L.mm_fill_weights_lane.restype = c_int
@@ -108,6 +113,12 @@ def lib():
     L.mm_selftest_convert.restype = c_int
     L.mm_selftest_convert.argtypes = [c_vp, c_int, c_vp, c_vp, c_vp]
     L.mm_dump_kernel_resources.restype = None
+    L.mm_probe_mfma_dot.restype = c_int
+    L.mm_probe_mfma_dot.argtypes = [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_vp]
+    L.mm_probe_stream_read.restype = c_int
+    L.mm_probe_stream_read.argtypes = [c_vp, ctypes.c_ulonglong, c_vp, c_int, c_vp]
+    L.mm_probe_mfma_rate.restype = c_int
+    L.mm_probe_mfma_rate.argtypes = [c_int, c_int, c_int, c_vp, c_vp]
     if L.mm_args_size() != ctypes.sizeof(MegaLaunchArgs):
         raise ImportError("MegaLaunchArgs mirror does not match the library's struct size")
     for name, *_ in MegaLaunchArgs._fields_:

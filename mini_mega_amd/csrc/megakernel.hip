@@ -3,9 +3,10 @@
 // extern "C" layer.  Reference counterpart: src/megakernel.cu:1-284 (launch
 // entry points) and test/mega_common.cuh:69-88,344-376 (geometry / args).
 //
-// Nothing here allocates, synchronises or reads the environment: every entry
-// point only validates its arguments and enqueues kernels on `stream`, so the
-// whole layer is capture-safe.  The workspace is caller-owned.
+// Nothing here allocates or reads the environment, and only read_status
+// synchronises: every launch entry point only validates its arguments and
+// enqueues kernels on `stream`, so the layer is capture-safe.  The workspace
+// is caller-owned.
 #include <cstddef>
 #include <cstdio>
 #include <cstring>
@@ -50,12 +51,17 @@ int check_dims(int topk, int E, int H, int I, int win_cap) {
 // The GEMMs' activation loaders address a row as a 32-bit byte offset
 // (token * H into x for L1, slot * I into the intermediate for L2), and slots
 // are int: capacities past those ranges are rejected rather than wrapped.
-int check_capacity(int64_t max_tokens, int topk, int H, int I) {
+// A work item records (index within its expert) | (items of the expert << 16)
+// and the big GEMMs decode it with & 0xffff and an arithmetic >> 16, so one
+// expert may hold at most 32767 items: ceil(max_tokens * topk / m_tile).
+int check_capacity(int64_t max_tokens, int topk, int H, int I, int win_cap) {
     if (max_tokens <= 0) return kErrBadDims;
     const int64_t pairs = max_tokens * topk;
     if (pairs > INT32_MAX || max_tokens * H > (int64_t(1) << 32) ||
         pairs * I > (int64_t(1) << 32))
         return kErrBadDims;
+    const int64_t m_tile = win_cap > 0 ? win_cap : auto_m_tile((int)max_tokens, topk, 0);
+    if ((pairs + m_tile - 1) / m_tile > 32767) return kErrBadDims;
     return kOk;
 }
 
@@ -74,7 +80,7 @@ int bind(const MegaLaunchArgs& a, Bound& b, bool need_weights) {
     if (a.rwk == nullptr || a.topk_idx == nullptr || a.self == nullptr) return kErrNullPointer;
     if (need_weights && (a.w1 == nullptr || a.w2 == nullptr)) return kErrNullPointer;
     if (a.tokens < 0) return kErrBadDims;
-    st = check_capacity(a.max_tokens, a.topk, a.hidden, a.intermediate);
+    st = check_capacity(a.max_tokens, a.topk, a.hidden, a.intermediate, a.win_cap);
     if (st != kOk) return st;
     if (a.tokens > a.max_tokens) return kErrTooManyTokens;
     if (a.R != 1 || a.rank != 0) return kErrUnsupported;
@@ -108,20 +114,27 @@ int launched(int st) {
     return hipPeekAtLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
+// bf16 x -> fp8 (+ per-128 UE8M0 scales) in the workspace (reference
+// x_fold_body, src/prologue.cuh:103-122).  Runs on every launch with bf16
+// input, also when skip_prologue reuses the routing: the tokens' routes may
+// repeat while x changes (the reference's kernel.cuh:69-101 folds x before
+// its skip_prologue test).
+void fold_x(const MegaLaunchArgs& a, const Bound& b, hipStream_t s) {
+    if (!a.in_bf16) return;
+    const size_t n8 = (size_t)a.tokens * a.hidden / 8;
+    if (n8 > 0)
+        hipLaunchKernelGGL(mm::quant_act_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                           s, reinterpret_cast<const uint16_t*>(a.self + a.x_off), a.tokens,
+                           a.hidden, b.ws + b.L.xq, a.w1_sf ? b.ws + b.L.xq_sf : nullptr);
+}
+
 int do_prelude(const MegaLaunchArgs& a, hipStream_t s) {
     Bound b;
     int st = bind(a, b, false);
     if (st != kOk) return st;
     const int E = a.num_experts, P = a.tokens * a.topk;
     int* status = at<int>(b, b.L.status);   // reset and written by route_scan_kernel
-    if (a.in_bf16) {
-        const size_t n8 = (size_t)a.tokens * a.hidden / 8;
-        if (n8 > 0)
-            hipLaunchKernelGGL(mm::quant_act_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256),
-                               0, s, reinterpret_cast<const uint16_t*>(a.self + a.x_off),
-                               a.tokens, a.hidden, b.ws + b.L.xq,
-                               a.w1_sf ? b.ws + b.L.xq_sf : nullptr);
-    }
+    fold_x(a, b, s);
     const int chunk = mm::route_chunk(P);
     const int nchunks = P > 0 ? (P + chunk - 1) / chunk : 0;
     int* hist = at<int>(b, b.L.chunk_hist);
@@ -219,8 +232,10 @@ int do_reduce(const MegaLaunchArgs& a, hipStream_t s) {
     Bound b;
     int st = bind(a, b, false);
     if (st != kOk) return st;
-    if (a.y == nullptr && a.y_bf16 == nullptr) return kErrNullPointer;
+    // an empty batch writes nothing, so it needs no output (a (0, H) tensor
+    // has a null data pointer)
     if (a.skip_combine || a.tokens == 0) return kOk;
+    if (a.y == nullptr && a.y_bf16 == nullptr) return kErrNullPointer;
     const int per_block = 256 * 8;
     const dim3 grid(a.tokens, (a.hidden + per_block - 1) / per_block);
     hipLaunchKernelGGL(mm::combine_kernel, grid, dim3(256), 0, s, at<uint16_t>(b, b.L.l2),
@@ -230,7 +245,14 @@ int do_reduce(const MegaLaunchArgs& a, hipStream_t s) {
 
 int do_compute(const MegaLaunchArgs& a, hipStream_t s) {
     int st = kOk;
-    if (!a.skip_prologue) st = do_prelude(a, s);
+    if (!a.skip_prologue) {
+        st = do_prelude(a, s);
+    } else {
+        // routing reused from the previous launch; x is still folded
+        Bound b;
+        st = bind(a, b, false);
+        if (st == kOk) fold_x(a, b, s);
+    }
     if (st == kOk) st = do_l1(a, s);
     if (st == kOk) st = do_l2(a, s);
     return st;
@@ -398,6 +420,19 @@ void dump_kernel_resources() {
 
 int last_error() { return g_last_error; }
 
+int read_status(const MegaLaunchArgs& a, int32_t* out, int n, hipStream_t s) {
+    if (out == nullptr) return record(kErrNullPointer);
+    if (n < 1 || n > mm::kStatusInts) return record(kErrBadDims);
+    Bound b;
+    int st = bind(a, b, false);
+    if (st != kOk) return record(st);
+    if (hipMemcpyAsync(out, b.ws + b.L.status, sizeof(int32_t) * (size_t)n, hipMemcpyDeviceToHost,
+                       s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return record(kErrLaunch);
+    return record(out[0] != 0 ? kErrDevice : kOk);
+}
+
 }  // namespace fp8mega
 
 // ------------------------------------------------------------------ C ABI --
@@ -428,7 +463,7 @@ int mm_layout(int max_tokens, int topk, int num_experts, int hidden, int interme
     if (!out) return fp8mega::kErrNullPointer;
     const int st = fp8mega::check_dims(topk, num_experts, hidden, intermediate, win_cap);
     if (st != fp8mega::kOk) return st;
-    const int cst = fp8mega::check_capacity(max_tokens, topk, hidden, intermediate);
+    const int cst = fp8mega::check_capacity(max_tokens, topk, hidden, intermediate, win_cap);
     if (cst != fp8mega::kOk) return cst;
     *out = fp8mega::layout(max_tokens, topk, num_experts, hidden, intermediate, win_cap);
     return fp8mega::kOk;
@@ -450,6 +485,11 @@ MM_WRAP(mm_launch_full, fp8mega::do_full)
 int mm_launch_dispatch(const MegaLaunchArgs* a, uint8_t* pool, void* stream) {
     if (!a) return fp8mega::kErrNullPointer;
     return fp8mega::record(fp8mega::do_dispatch(*a, pool, (hipStream_t)stream));
+}
+
+int mm_read_status(const MegaLaunchArgs* a, int* out, int n, void* stream) {
+    if (!a) return fp8mega::kErrNullPointer;
+    return fp8mega::read_status(*a, out, n, (hipStream_t)stream);
 }
 
 int mm_launch_empty(int grid, int threads, long long smem, void* stream) {

@@ -29,6 +29,7 @@ constexpr int kBigMaxKT = 64;       // large-M GEMMs: K / 128 <= 64 (H, I <= 819
 constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 workgroup
 constexpr int kL2BlockN = 256;      // output channels per L2 workgroup
 constexpr int kStatusInts = 64;     // workspace status words
+constexpr int kStatusItemOverflow = fp8mega::kStatusItemOverflow;
 constexpr int kCutsL1 = 16;         // status[16..24]: XCD unit ranges of the L1 big GEMM
 constexpr int kCutsL2 = 32;         // status[32..40]: the same for L2
 

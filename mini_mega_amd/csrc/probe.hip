@@ -1,0 +1,135 @@
+// probe.hip -- measurement kernels (no reference counterpart): the
+// accumulation precision of gfx950's fp8 and bf16 MFMAs on a dot-product
+// block, a read-only HBM stream of known bytes, and MFMA issue-rate loops.
+// They back the numeric choice of the GEMMs (bf16 MFMA after an exact fp8 ->
+// bf16 conversion) and the measured peaks the benchmark reports beside the
+// datasheet ones.  Nothing on the layer's path calls them.
+#include "mm_kernels.h"
+
+namespace mm {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+// out[r][n] = sum_k dec(a[r][k]) * dec(b[n][k]) for r < 16, one 64-lane
+// workgroup per 16 columns n.  a: [16][K], b: [N][K] fp8 e4m3 row-major,
+// K % 128 == 0.  mode 0: v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales),
+// one accumulator chained over K; mode 1: v_mfma_f32_16x16x32_bf16 after
+// the exact fp8 -> bf16 conversion the layer's GEMMs use.
+__global__ void __launch_bounds__(64)
+mfma_dot_probe_kernel(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, int K,
+                      int mode, float* __restrict__ out, int N) {
+    const int l = threadIdx.x, n0 = blockIdx.x * 16;
+    const uint8_t* ar = a + (size_t)(l & 15) * K;
+    const uint8_t* br = b + (size_t)(n0 + (l & 15)) * K;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < K; kb += 128) {
+        const int k0 = kb + 32 * (l >> 4);
+        const v4i a0 = load16(ar + k0), a1 = load16(ar + k0 + 16);
+        const v4i b0 = load16(br + k0), b1 = load16(br + k0 + 16);
+        if (mode == 0) {
+            const v8i av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            const v8i bv = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+            acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, 0, 0, 0, 127, 0,
+                                                                   127);
+        } else {
+            // lane L holds k in [k0, k0 + 32): bytes 8q .. 8q+7 are its operand
+            // of the q-th 16x16x32 MFMA of this 128-k step, as in the GEMMs
+            const int aw[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            const int bw[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                acc = mfma_bf16(fp8x8_to_bf16(aw[2 * q], aw[2 * q + 1], 1.0f),
+                                fp8x8_to_bf16(bw[2 * q], bw[2 * q + 1], 1.0f), acc);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[(size_t)(4 * (l >> 4) + i) * N + n0 + (l & 15)] = acc[i];
+}
+
+// Reads `n16` 16-byte words once (non-temporal, grid-stride) and writes one
+// XOR per thread to sink[global thread id], so the loads cannot be dropped.
+__global__ void __launch_bounds__(256)
+stream_read_kernel(const uint8_t* __restrict__ src, size_t n16, uint32_t* __restrict__ sink) {
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    uint32_t x = 0;
+    size_t i = tid;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const v4i v0 = load16_stream(src + i * 16);
+        const v4i v1 = load16_stream(src + (i + stride) * 16);
+        const v4i v2 = load16_stream(src + (i + 2 * stride) * 16);
+        const v4i v3 = load16_stream(src + (i + 3 * stride) * 16);
+        x ^= (uint32_t)(v0[0] ^ v0[1] ^ v0[2] ^ v0[3] ^ v1[0] ^ v1[1] ^ v1[2] ^ v1[3]);
+        x ^= (uint32_t)(v2[0] ^ v2[1] ^ v2[2] ^ v2[3] ^ v3[0] ^ v3[1] ^ v3[2] ^ v3[3]);
+    }
+    for (; i < n16; i += stride) {
+        const v4i v = load16_stream(src + i * 16);
+        x ^= (uint32_t)(v[0] ^ v[1] ^ v[2] ^ v[3]);
+    }
+    sink[tid] = x;
+}
+
+// MFMA issue rate: every wave runs `iters` rounds of 8 independent
+// accumulator chains (mode 0: 16x16x32 bf16, mode 1: 16x16x128 fp8 with unit
+// scales) from registers; sink[wave] keeps one lane's sum.
+__global__ void __launch_bounds__(256)
+mfma_rate_kernel(int mode, int iters, float* __restrict__ sink) {
+    const int l = threadIdx.x & 63;
+    v4f acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (mode == 0) {
+        v8bf x;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = (__bf16)(0.001f * (float)((l + j) & 7));
+        for (int it = 0; it < iters; ++it)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] = mfma_bf16(x, x, acc[c]);
+    } else {
+        v8i x;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = 0x20202020 + ((l + j) & 7);
+        for (int it = 0; it < iters; ++it)
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                acc[c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, x, acc[c], 0, 0, 0,
+                                                                          127, 0, 127);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
+    if (l == 0) sink[(size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)] = s;
+}
+
+}  // namespace mm
+
+extern "C" {
+
+int mm_probe_mfma_dot(const uint8_t* a, const uint8_t* b, int K, int N, int mode, float* out,
+                      void* stream) {
+    if (!a || !b || !out) return fp8mega::kErrNullPointer;
+    if (K <= 0 || K % 128 || N <= 0 || N % 16 || (mode != 0 && mode != 1))
+        return fp8mega::kErrBadDims;
+    hipLaunchKernelGGL(mm::mfma_dot_probe_kernel, dim3(N / 16), dim3(64), 0, (hipStream_t)stream,
+                       a, b, K, mode, out, N);
+    return hipPeekAtLastError() == hipSuccess ? fp8mega::kOk : fp8mega::kErrLaunch;
+}
+
+int mm_probe_stream_read(const uint8_t* src, unsigned long long bytes, uint32_t* sink, int grid,
+                         void* stream) {
+    if (!src || !sink) return fp8mega::kErrNullPointer;
+    if (bytes % 16 || grid <= 0) return fp8mega::kErrBadDims;
+    hipLaunchKernelGGL(mm::stream_read_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, src,
+                       (size_t)(bytes / 16), sink);
+    return hipPeekAtLastError() == hipSuccess ? fp8mega::kOk : fp8mega::kErrLaunch;
+}
+
+int mm_probe_mfma_rate(int mode, int iters, int grid, float* sink, void* stream) {
+    if (!sink) return fp8mega::kErrNullPointer;
+    if ((mode != 0 && mode != 1) || iters <= 0 || grid <= 0) return fp8mega::kErrBadDims;
+    hipLaunchKernelGGL(mm::mfma_rate_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, mode,
+                       iters, sink);
+    return hipPeekAtLastError() == hipSuccess ? fp8mega::kOk : fp8mega::kErrLaunch;
+}
+
+}  // extern "C"

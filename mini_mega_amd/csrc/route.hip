@@ -98,11 +98,10 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     }
     // E <= kMaxExperts = kScanThreads: one expert per thread.
     const int e = threadIdx.x;
-    int cnt = 0;
+    int cnt = 0, run = 0;
     if (e < E) {
         // exclusive prefix over chunks (uncapped rank base), 8 chunks' loads
         // in flight at a time
-        int run = 0;
         for (int c0 = 0; c0 < nchunks; c0 += 8) {
             int h[8];
 #pragma unroll
@@ -120,6 +119,10 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
         cnt = min(run, cap);
         counts[e] = cnt;
     }
+    // pairs with an id in [0, E) before the slot cap (the rest of P had ids
+    // outside [0, E))
+    int valid = 0;
+    (void)block_exclusive_scan(run, smem, &valid);
     int slots = 0;
     const int off = block_exclusive_scan(cnt, smem, &slots);
     if (e < E) offsets[e] = off;
@@ -142,7 +145,9 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     if (threadIdx.x == 0) {
         status[1] = min(nitems, max_items);
         status[2] = slots;
-        if (nitems > max_items) atomicOr(&status[0], 1);
+        status[3] = valid - slots;   // pairs dropped by the slot capacity
+        status[4] = P - valid;       // pairs whose expert id is outside [0, E)
+        if (nitems > max_items) atomicOr(&status[0], kStatusItemOverflow);
     }
     // XCD ranges of the big GEMMs' units (nb blocks per item; an expert's
     // nb * nm units are contiguous in the kernels' numbering).  Modelled cost

@@ -209,6 +209,40 @@ class SymmBuffer:
             a.ffn_ue8m0 = 1
         return a
 
+    def make_reduce_args(self, num_tokens: int, y_bf16: torch.Tensor) -> MegaLaunchArgs:
+        """MegaLaunchArgs for launch_reduce alone: the reduce reads the
+        workspace (L2 rows, slots) and the topk weights, no layer weights."""
+        a = MegaLaunchArgs()
+        a.tokens = int(num_tokens)
+        a.win_cap = self.expert_window
+        a.rwk = self.workspace.data_ptr()
+        a.self = self.buffer.data_ptr()
+        a.x_off = self._x_off
+        a.weights_off = self._w_off
+        a.topk_idx = self.topk_idx.data_ptr()
+        a.in_bf16 = 1 if self.mma_type == "bf16xfp8" else 0
+        a.y = self._y_fp32.data_ptr() if self.write_fp32_y else None
+        a.y_bf16 = y_bf16.data_ptr()
+        a.num_experts, a.topk = self.num_experts, self.num_topk
+        a.hidden, a.intermediate = self.hidden, self.intermediate_hidden
+        a.max_tokens = self.num_max_tokens_per_rank
+        a.workspace_bytes = int(self.layout.total)
+        return a
+
+    def device_status(self) -> dict:
+        """The device status words of the last launch on this buffer (through
+        mm_read_status, which synchronises the current stream): error bits,
+        work items, routed slots, pairs dropped by the slot capacity and pairs
+        with an expert id outside [0, num_experts)."""
+        import ctypes as _c
+        a = self.make_reduce_args(0, self.workspace)
+        out = (_c.c_int * 5)()
+        rc = lib().mm_read_status(_c.byref(a), out, 5, _stream_ptr())
+        if rc not in (0, _lib.ERR_DEVICE):
+            check("mm_read_status", rc)
+        return dict(error=int(out[0]), items=int(out[1]), slots=int(out[2]),
+                    dropped_by_capacity=int(out[3]), invalid_ids=int(out[4]))
+
     def destroy(self):
         self.buffer = self.workspace = self._y_fp32 = None
 
@@ -386,6 +420,20 @@ def _check_common(fn: str, sym_buffer: SymmBuffer, activation: str):
         raise ValueError(f"fp8xfp8 requires activation='swiglu', got {activation!r}")
 
 
+def _check_output(fn: str, y: torch.Tensor, sym_buffer: SymmBuffer, num_tokens: int) -> None:
+    """y must be the contiguous bf16 [num_tokens, hidden] tensor on the buffer's
+    device: the combine kernel writes num_tokens * hidden values through its
+    pointer (the reference copies into y, which raises on a mismatch,
+    mega/__init__.py:655)."""
+    if not isinstance(y, torch.Tensor) or y.dtype != torch.bfloat16 or not y.is_contiguous():
+        raise TypeError(f"{fn}: y must be a contiguous bfloat16 tensor")
+    if y.dim() != 2 or int(y.shape[1]) != sym_buffer.hidden or int(y.shape[0]) < num_tokens:
+        raise ValueError(f"{fn}: y has shape {tuple(y.shape)}, needs ({num_tokens}, "
+                         f"{sym_buffer.hidden})")
+    if num_tokens > 0 and (y.device.type != "cuda" or y.device.index != sym_buffer.device):
+        raise ValueError(f"{fn}: y is on {y.device}, the buffer on cuda:{sym_buffer.device}")
+
+
 def fp8_mega_moe(y: torch.Tensor, l1_weights, l2_weights, sym_buffer: SymmBuffer,
                  cumulative_local_expert_recv_stats=None, activation: str = "swiglu",
                  activation_clamp=None, expert_window: Optional[int] = None) -> None:
@@ -397,13 +445,14 @@ def fp8_mega_moe(y: torch.Tensor, l1_weights, l2_weights, sym_buffer: SymmBuffer
     if num_tokens > sym_buffer.num_max_tokens_per_rank:
         raise ValueError(f"num_tokens={num_tokens} exceeds capacity "
                          f"{sym_buffer.num_max_tokens_per_rank}")
-    if y.dtype != torch.bfloat16 or not y.is_contiguous():
-        raise TypeError("y must be a contiguous bfloat16 tensor")
+    _check_output("fp8_mega_moe", y, sym_buffer, num_tokens)
     if expert_window is not None and int(expert_window) != sym_buffer.expert_window:
         raise ValueError("expert_window is fixed when the SymmBuffer is built")
-    a = sym_buffer.make_args(num_tokens, l1_weights, l2_weights, y_bf16=y)
+    a = sym_buffer.make_args(num_tokens, l1_weights, l2_weights,
+                             y_bf16=y if num_tokens > 0 else None)
     check("mm_launch_full", lib().mm_launch_full(ctypes.byref(a), _stream_ptr()))
     sym_buffer.launch_count += 1
+    sym_buffer._last_compute_tokens = num_tokens
     if cumulative_local_expert_recv_stats is not None:
         cumulative_local_expert_recv_stats.add_(sym_buffer.counts()[
             :cumulative_local_expert_recv_stats.numel()].to(
@@ -412,31 +461,50 @@ def fp8_mega_moe(y: torch.Tensor, l1_weights, l2_weights, sym_buffer: SymmBuffer
 
 def fp8_mega_moe_compute(l1_weights, l2_weights, sym_buffer: SymmBuffer, num_tokens: int,
                          activation: str = "swiglu", activation_clamp=None,
-                         expert_window: Optional[int] = None) -> None:
-    """Routing + L1 + L2 without the reduce (reference :658-693)."""
+                         expert_window: Optional[int] = None, skip_prologue: int = 0) -> None:
+    """Routing + L1 + L2 without the reduce (reference :658-693).  The L2 rows
+    stay in the buffer's workspace until fp8_mega_moe_reduce; kernels that do
+    not touch this buffer may run in between.  skip_prologue=1 reuses the
+    routing of the buffer's previous launch (same topk_idx and num_tokens;
+    the reference's graph-node option, src/megakernel.h:106): only x is
+    folded again for a bf16xfp8 buffer."""
     _check_common("fp8_mega_moe_compute", sym_buffer, activation)
     num_tokens = int(num_tokens)
     if num_tokens < 0 or num_tokens > sym_buffer.num_max_tokens_per_rank:
         raise ValueError(f"num_tokens={num_tokens} exceeds capacity "
                          f"{sym_buffer.num_max_tokens_per_rank}")
-    a = sym_buffer.make_args(num_tokens, l1_weights, l2_weights)
-    sym_buffer._last_weights = (l1_weights, l2_weights)
+    if expert_window is not None and int(expert_window) != sym_buffer.expert_window:
+        raise ValueError("expert_window is fixed when the SymmBuffer is built")
+    if skip_prologue and getattr(sym_buffer, "_last_compute_tokens", None) != num_tokens:
+        raise ValueError("skip_prologue reuses the previous launch's routing: it needs a "
+                         "previous launch with the same num_tokens")
+    a = sym_buffer.make_args(num_tokens, l1_weights, l2_weights, skip_prologue=skip_prologue)
     check("mm_launch_compute", lib().mm_launch_compute(ctypes.byref(a), _stream_ptr()))
     sym_buffer.launch_count += 1
+    sym_buffer._last_compute_tokens = num_tokens
 
 
 def fp8_mega_moe_reduce(y: torch.Tensor, sym_buffer: SymmBuffer,
                         num_tokens: Optional[int] = None) -> None:
-    """Top-k weighted reduce into y (bf16) after fp8_mega_moe_compute
-    (reference :696-712)."""
+    """Top-k weighted reduce into y (bf16) of the buffer's last
+    fp8_mega_moe_compute (reference :696-712).  The reduce reads only the
+    workspace's L2 rows and slots and the buffer's topk_weights, so it needs no
+    weights; num_tokens (default y.shape[0]) may not exceed the token count of
+    that compute."""
+    if sym_buffer.mma_type not in _SUPPORTED_MMA_TYPES:
+        raise ValueError(f"fp8_mega_moe_reduce requires fp8xfp8/bf16xfp8 SymmBuffer, got "
+                         f"{sym_buffer.mma_type!r}")
     nt = int(num_tokens) if num_tokens is not None else int(y.shape[0])
     if nt <= 0 or nt > sym_buffer.num_max_tokens_per_rank:
         raise ValueError(f"num_tokens={nt} out of range "
                          f"(capacity {sym_buffer.num_max_tokens_per_rank})")
-    l1, l2 = getattr(sym_buffer, "_last_weights", (None, None))
-    if l1 is None:
+    last = getattr(sym_buffer, "_last_compute_tokens", None)
+    if last is None:
         raise RuntimeError("fp8_mega_moe_reduce needs a preceding fp8_mega_moe_compute")
-    a = sym_buffer.make_args(nt, l1, l2, y_bf16=y)
+    if nt > last:
+        raise ValueError(f"num_tokens={nt} exceeds the {last} tokens of the last compute")
+    _check_output("fp8_mega_moe_reduce", y, sym_buffer, nt)
+    a = sym_buffer.make_reduce_args(nt, y)
     check("mm_launch_reduce", lib().mm_launch_reduce(ctypes.byref(a), _stream_ptr()))
 
 

@@ -35,6 +35,14 @@
 static int g_acc64 = 0;
 ORC_API void orc_set_acc64(int on) { g_acc64 = on; }
 
+/* Planted mistakes, for the tests that show the oracle's pins are sensitive
+ * (0 = none, the only value outside those tests): 1 = the up rows of L1 take
+ * their gate rows' 128-row scale block; 2 = the W2 scale block index is
+ * transposed ((k/128, n/128) instead of (n/128, k/128)); 3 = the ffn rows
+ * take the scale of the next 128-column block. */
+static int g_mutation = 0;
+ORC_API void orc_set_mutation(int m) { g_mutation = m; }
+
 /* ------------------------------------------------------------ E4M3 decode --
  * src/bench_check.cuh:327-358: exp=0 -> +-(m/8)*2^-6; exp 1..15 ->
  * +-(1+m/8)*2^(exp-7); 0x7F/0xFF -> NaN; max finite 448 = 0x7E. */
@@ -304,7 +312,8 @@ ORC_API void orc_l1_rows(const uint8_t* x, const uint8_t* xsf, int rows, const u
         if (w1sf)
             for (int b = 0; b < kb; ++b) {
                 const float sg = ue8m0_scale(w1sf[(size_t)(grow / 128) * kb + b]);
-                const float su = ue8m0_scale(w1sf[(size_t)(urow / 128) * kb + b]);
+                const int ub = g_mutation == 1 ? grow / 128 : urow / 128;
+                const float su = ue8m0_scale(w1sf[(size_t)ub * kb + b]);
                 for (int k = b * 128; k < b * 128 + 128; ++k) {
                     wg[k] *= sg;
                     wu[k] *= su;
@@ -361,14 +370,17 @@ ORC_API void orc_l2_rows(const uint8_t* ffn, const uint8_t* fsf, int rows, const
     for (int r = 0; r < rows; ++r)
         for (int k = 0; k < I; ++k) {
             float v = g_e4m3[ffn[(size_t)r * I + k]];
-            if (fsf) v *= ue8m0_scale(fsf[(size_t)r * kb + k / 128]);
+            const int fb = g_mutation == 3 ? (k / 128 + 1) % kb : k / 128;
+            if (fsf) v *= ue8m0_scale(fsf[(size_t)r * kb + fb]);
             ad[(size_t)r * I + k] = v;
         }
     for (int n = 0; n < H; ++n) {
         for (int k = 0; k < I; ++k) wr[k] = g_e4m3[w2e[(size_t)n * I + k]];
         if (w2sf)
             for (int b = 0; b < kb; ++b) {
-                const float sb = ue8m0_scale(w2sf[(size_t)(n / 128) * kb + b]);
+                const size_t wi = g_mutation == 2 ? (size_t)b * (H / 128) + n / 128
+                                                  : (size_t)(n / 128) * kb + b;
+                const float sb = ue8m0_scale(w2sf[wi]);
                 for (int k = b * 128; k < b * 128 + 128; ++k) wr[k] *= sb;
             }
         for (int r = 0; r < rows; ++r) {

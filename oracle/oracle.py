@@ -62,6 +62,7 @@ def lib():
         L.orc_l2_rows.argtypes = [vp, vp, i32, vp, vp, i32, i32, vp]
         L.orc_reduce.argtypes = [vp, vp, vp, i32, i32, i32, vp, vp]
         L.orc_set_acc64.argtypes = [i32]
+        L.orc_set_mutation.argtypes = [i32]
         L.orc_layer_slots.restype = i32
         L.orc_layer_slots.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32,
                                       i32, i32, vp, vp, vp, vp, i32]
@@ -162,6 +163,12 @@ def route(topk_idx: np.ndarray, E: int, cap: int | None = None):
     pair_pos = np.empty(T * K, np.int32)
     lib().orc_route(_p(idx), T, K, E, cap, _p(counts), _p(offsets), _p(perm), _p(pair_pos))
     return counts, offsets, perm[: offsets[E]], pair_pos
+
+
+def set_mutation(m: int) -> None:
+    """Plants a known mistake in the oracle (tests of the pins' sensitivity
+    only; 0 restores the faithful restatement)."""
+    lib().orc_set_mutation(int(m))
 
 
 def l1_rows(x, xsf, w1e, w1sf, G: int):

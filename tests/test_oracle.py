@@ -296,3 +296,265 @@ def test_layer_chain_small_against_fp64_model():
             y[tok] += ob * wts[tok, k]
     rms = np.sqrt(np.mean(y ** 2))
     assert np.abs(ref["y"] - y).max() <= 2e-2 * rms
+
+
+# ------------------------------------------------ block-scaled (UE8M0) path --
+# The scaled oracle (x_sf per token per 128 columns, w1_sf / w2_sf per 128x128
+# block of the paired / plain weight matrix, ffn requantised per 128 columns)
+# checked against float64 dequantise-then-GEMM restatements of
+# torch/tests/test_fp8_mega_moe.py:28-48 with the casts of
+# torch/mxmegakernel/utils/math.py:13-72.  Every scale below is a random
+# non-unit power of two; gate and up rows of one hidden column sit in
+# different 128-row blocks, so a wrong block index changes the result by a
+# power of two, far outside the tolerances.
+
+def _dec64():
+    return orc.e4m3_decode_table().astype(np.float64)
+
+
+def _scale_of(sf):
+    return np.ldexp(1.0, sf.astype(np.int32) - 127)
+
+
+def _deq_rows(q, sf):
+    """[rows][K] bytes with per-row per-128 scales [rows][K/128] -> float64."""
+    return _dec64()[q] * np.repeat(_scale_of(sf), 128, axis=1)
+
+
+def _deq_blocks(q, sf):
+    """[N][K] bytes with 128x128 block scales [N/128][K/128] -> float64."""
+    s = _scale_of(sf)
+    return _dec64()[q] * np.repeat(np.repeat(s, 128, axis=0), 128, axis=1)
+
+
+def _paired_rows(I, G):
+    h = np.arange(I)
+    grow = (h // G) * 2 * G + h % G
+    return grow, grow + G
+
+
+def _silu64(g):
+    return g / (1.0 + np.exp(-np.clip(g, -700.0, 700.0)))
+
+
+def _l1_model(xq, xsf, w1q, w1sf, G, up_block_of=None):
+    """h = silu(g) * u in float64, with g, u and the sums of |terms| that bound
+    their accumulation error.  up_block_of (a planted mistake, used only to
+    show the comparison's sensitivity) maps each up row to the 128-row block
+    whose scale it is given."""
+    I = w1q.shape[0] // 2
+    xd = _deq_rows(xq, xsf)
+    wd = _deq_blocks(w1q, w1sf)
+    grow, urow = _paired_rows(I, G)
+    if up_block_of is not None:
+        raw = _dec64()[w1q]
+        s = _scale_of(w1sf)
+        wu = raw[urow] * np.repeat(s[up_block_of(urow)], 128, axis=1)
+    else:
+        wu = wd[urow]
+    g = xd @ wd[grow].T
+    u = xd @ wu.T
+    return (_silu64(g) * u, dict(g=g, u=u, ag=np.abs(xd) @ np.abs(wd[grow]).T,
+                                 au=np.abs(xd) @ np.abs(wu).T))
+
+
+def _scaled_l1_case(rows, H, I, seed):
+    r = np.random.default_rng(seed)
+    xq = _rand_fp8((rows, H), 1.0)
+    w1q = _rand_fp8((2 * I, H), 0.05)
+    xsf = r.integers(121, 134, size=(rows, H // 128)).astype(np.uint8)
+    w1sf = r.integers(116, 138, size=(2 * I // 128, H // 128)).astype(np.uint8)
+    return xq, xsf, w1q, w1sf
+
+
+@pytest.fixture
+def mutation():
+    """Sets an oracle mutation for one test and always restores the faithful
+    oracle afterwards."""
+    yield orc.set_mutation
+    orc.set_mutation(0)
+
+
+def _l1_within_bound(got, want, m, H):
+    # sequential fp32 sums of H terms: |err(g)| <= H * 2^-24 * sum|terms|
+    # (likewise u); h = silu(g) * u moves by at most 1.1 |u| err(g) +
+    # |silu(g)| err(u) (|silu'| <= 1.1), plus the final fp32 roundings
+    c = H * 2.0 ** -24
+    bound = 1.1 * np.abs(m["u"]) * c * m["ag"] + np.abs(_silu64(m["g"])) * c * m["au"]
+    return np.abs(got - want) <= bound + 4 * 2.0 ** -24 * np.abs(want)
+
+
+@pytest.mark.parametrize("H,I,G", [(384, 256, 256), (256, 512, 256), (512, 128, 128)])
+def test_l1_scaled_matches_fp64_dequant_gemm(H, I, G, mutation):
+    rows = 6
+    xq, xsf, w1q, w1sf = _scaled_l1_case(rows, H, I, seed=H + I)
+    want, m = _l1_model(xq, xsf, w1q, w1sf, G)
+    got = orc.l1_rows(xq, xsf, w1q, w1sf, G).astype(np.float64)
+    ok = _l1_within_bound(got, want, m, H)
+    assert ok.all(), f"max |d| {np.abs(got - want).max():.3e}"
+    # the pin catches an oracle whose up rows take their gate rows' scale block
+    mutation(1)
+    bad = orc.l1_rows(xq, xsf, w1q, w1sf, G).astype(np.float64)
+    assert np.mean(~_l1_within_bound(bad, want, m, H)) > 0.5
+
+
+def test_l1_scaled_row_and_block_scales_are_independent():
+    """One x row's block scaled by 2^3 scales exactly that row's g and u
+    contributions from those 128 columns; one W1 block scaled by 2^-2 scales
+    exactly the rows of that block (power-of-two scales are exact)."""
+    H, I, G = 256, 256, 256
+    xq = _rand_fp8((3, H), 1.0)
+    w1q = _rand_fp8((2 * I, H), 0.05)
+    xsf = np.full((3, H // 128), 127, np.uint8)
+    w1sf = np.full((2 * I // 128, H // 128), 127, np.uint8)
+    base = orc.l1_rows(xq, xsf, w1q, w1sf, G)
+    # gate rows 0..127 (block 0) get 2^-2 on both k-blocks: g of h = 0..127
+    # scales by 1/4 exactly, so h = silu(g/4) * u, which the model reproduces
+    w1sf2 = w1sf.copy()
+    w1sf2[0, :] = 125
+    got = orc.l1_rows(xq, xsf, w1q, w1sf2, G).astype(np.float64)
+    want, _ = _l1_model(xq, xsf, w1q, w1sf2, G)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(got[:, 128:], base[:, 128:].astype(np.float64))
+    assert not np.allclose(got[:, :128], base[:, :128], rtol=1e-3)
+
+
+@pytest.mark.parametrize("H,I", [(384, 256), (256, 512)])
+def test_l2_scaled_matches_fp64_dequant_gemm(H, I, mutation):
+    rows = 5
+    r = np.random.default_rng(H * I)
+    fq = _rand_fp8((rows, I), 1.0)
+    fsf = r.integers(118, 136, size=(rows, I // 128)).astype(np.uint8)
+    w2q = _rand_fp8((H, I), 0.05)
+    w2sf = r.integers(116, 138, size=(H // 128, I // 128)).astype(np.uint8)
+    fd, wd = _deq_rows(fq, fsf), _deq_blocks(w2q, w2sf)
+    want = fd @ wd.T
+    terms = np.abs(fd) @ np.abs(wd).T     # sequential fp32: |err| <= I 2^-24 terms
+    got = orc.l2_rows(fq, fsf, w2q, w2sf).astype(np.float64)
+    assert np.all(np.abs(got - want) <= I * 2.0 ** -24 * terms)
+    # the pin catches ffn scales taken from the neighbouring 128-column block
+    mutation(3)
+    bad = orc.l2_rows(fq, fsf, w2q, w2sf).astype(np.float64)
+    assert np.mean(np.abs(bad - want) > I * 2.0 ** -24 * terms) > 0.5
+
+
+def test_l2_scaled_block_index_not_transposed(mutation):
+    """Square 2x2 block grid with distinct scales: W2 block (n/128, k/128)
+    versus its transpose (k/128, n/128) differ on the off-diagonal blocks."""
+    H = I = 256
+    fq = _rand_fp8((4, I), 1.0)
+    fsf = np.full((4, 2), 127, np.uint8)
+    w2q = _rand_fp8((H, I), 0.05)
+    w2sf = np.array([[127, 131], [123, 127]], np.uint8)   # 2^0, 2^4 / 2^-4, 2^0
+    fd, wd = _deq_rows(fq, fsf), _deq_blocks(w2q, w2sf)
+    want = fd @ wd.T
+    terms = np.abs(fd) @ np.abs(wd).T
+    got = orc.l2_rows(fq, fsf, w2q, w2sf).astype(np.float64)
+    assert np.all(np.abs(got - want) <= I * 2.0 ** -24 * terms)
+    mutation(2)
+    bad = orc.l2_rows(fq, fsf, w2q, w2sf).astype(np.float64)
+    assert np.abs(bad - want).max() > 1e-2 * np.abs(want).max()
+
+
+def _torch_per_token_cast_ue8m0(h: np.ndarray):
+    """utils/math.py:13-16,23-47 (ceil_to_ue8m0, per_token_cast_to_fp8 with
+    use_ue8m0=True, gran 128) in torch float32 on the CPU: returns fp8 bytes
+    and UE8M0 exponent bytes."""
+    x = torch.from_numpy(np.ascontiguousarray(h, np.float32))
+    m, n = x.shape
+    xv = x.view(m, n // 128, 128)
+    amax = xv.abs().float().amax(dim=2).clamp(1e-4)
+    sf = amax / 448.0
+    bits = sf.abs().float().view(torch.int32)
+    exp = ((bits >> 23) & 0xFF) + (bits & 0x7FFFFF).bool().int()
+    sf = (exp.clamp(1, 254) << 23).view(torch.float32)
+    q = (xv * (1.0 / sf.unsqueeze(2))).to(torch.float8_e4m3fn).view(m, n)
+    return q.view(torch.uint8).numpy(), ((sf.view(torch.int32) >> 23) & 0xFF).to(
+        torch.uint8).numpy()
+
+
+@pytest.mark.parametrize("scale", [1e-3, 0.7, 300.0])
+def test_quant_ffn_scaled_equals_torch_recipe(scale):
+    h = (rng.standard_normal((12, 512)) * scale).astype(np.float32)
+    h[3, :128] = 0.0                      # an all-zero block: amax clamps to 1e-4
+    h[5, 128:256] *= 1e-6                 # a tiny block next to normal ones
+    q, sf = orc.quant_ffn(h, True)
+    tq, tsf = _torch_per_token_cast_ue8m0(h)
+    assert np.array_equal(sf, tsf)
+    assert np.array_equal(q, tq)
+
+
+def _chain_model(x, xsf, w1, w1sf, w2, w2sf, idx, wts, G, ffn_override=None):
+    """Whole scaled layer in float64 / torch casts, the reference() of
+    torch/tests/test_fp8_mega_moe.py:28-48 with block-scaled operands: per
+    (token, k) h = silu(x W1g^T) * (x W1u^T), per_token_cast_to_fp8(h, ue8m0),
+    out = bf16(deq(ffn) W2^T), y += out * w.  ffn_override[(t, k)] = (q, sf)
+    feeds given ffn bytes to L2 instead (a staged check)."""
+    T, K = idx.shape
+    E = w1.shape[0]
+    H = x.shape[1]
+    y = np.zeros((T, H), np.float64)
+    ffn = {}
+    for t in range(T):
+        for k in range(K):
+            e = int(idx[t, k])
+            if not (0 <= e < E):
+                continue
+            if ffn_override is not None:
+                q, sf = ffn_override[(t, k)]
+            else:
+                h, _ = _l1_model(x[t:t + 1], xsf[t:t + 1], w1[e], w1sf[e], G)
+                q, sf = _torch_per_token_cast_ue8m0(h.astype(np.float32))
+            ffn[(t, k)] = (q, sf)
+            o = _deq_rows(q, sf) @ _deq_blocks(w2[e], w2sf[e]).T
+            ob = torch.from_numpy(o.astype(np.float32)).to(torch.bfloat16).float().numpy()
+            y[t] += ob[0].astype(np.float64) * float(wts[t, k])
+    return y, ffn
+
+
+def test_layer_scaled_chain_against_fp64_model(mutation):
+    """The scaled oracle chain (routing, L1 with x_sf / w1_sf, UE8M0 ffn
+    requant, L2 with ffn / w2 scales, bf16, reduce) against the float64
+    reference() model: ffn bytes and scales (almost all equal: the model sums
+    in float64, the oracle in sequential fp32), the staged L2 + reduce on the
+    oracle's own ffn (bf16 rows within one ulp), and y at the end-to-end bar."""
+    E, K, H, I, T, G = 4, 2, 256, 256, 10, 256
+    r = np.random.default_rng(77)
+    x = _rand_fp8((T, H), 1.0)
+    xsf = r.integers(122, 132, size=(T, H // 128)).astype(np.uint8)
+    w1 = np.stack([_rand_fp8((2 * I, H), 0.05) for _ in range(E)])
+    w1sf = r.integers(118, 136, size=(E, 2 * I // 128, H // 128)).astype(np.uint8)
+    w2 = np.stack([_rand_fp8((H, I), 0.05) for _ in range(E)])
+    w2sf = r.integers(118, 136, size=(E, H // 128, I // 128)).astype(np.uint8)
+    idx = np.stack([r.permutation(E)[:K] for _ in range(T)]).astype(np.int64)
+    idx[2, 1] = E + 1                      # an invalid id: no contribution
+    wts = r.random((T, K)).astype(np.float32)
+    ref = orc.layer(x, xsf, w1, w1sf, w2, w2sf, idx, wts, E=E, G=G, scaled=True)
+    y_model, ffn_model = _chain_model(x, xsf, w1, w1sf, w2, w2sf, idx, wts, G)
+    # ffn: slot of pair (t, k) is pair_pos[t*K + k]
+    flips = total = sf_diff = 0
+    override = {}
+    for (t, k), (q, sf) in ffn_model.items():
+        s = int(ref["pair_pos"][t * K + k])
+        assert s >= 0
+        oq, osf = ref["ffn"][s], ref["ffn_sf"][s]
+        flips += int(np.sum(oq != q[0]))
+        total += q.size
+        sf_diff += int(np.sum(osf != sf[0]))
+        override[(t, k)] = (oq[None, :], osf[None, :])
+    assert sf_diff == 0, "ffn block scales differ from the torch recipe"
+    assert flips <= max(1, total // 500), f"{flips} of {total} ffn bytes differ"
+    # staged: L2 + reduce on the oracle's own ffn
+    y_staged, _ = _chain_model(x, xsf, w1, w1sf, w2, w2sf, idx, wts, G, ffn_override=override)
+    rms = float(np.sqrt(np.mean(y_staged ** 2)))
+    assert np.abs(ref["y"] - y_staged).max() <= 2 ** -7 * rms
+    # end to end
+    rms = float(np.sqrt(np.mean(y_model ** 2)))
+    err = float(np.abs(ref["y"] - y_model).max())
+    cos = float((ref["y"] * y_model).sum() / (np.linalg.norm(ref["y"]) * np.linalg.norm(y_model)))
+    assert err <= 2e-2 * rms and cos >= 0.9995, (err / rms, cos)
+    # the end-to-end bar rejects an oracle with any of the planted scale slips
+    for m in (1, 2, 3):
+        mutation(m)
+        bad = orc.layer(x, xsf, w1, w1sf, w2, w2sf, idx, wts, E=E, G=G, scaled=True)["y"]
+        assert np.abs(bad - y_model).max() > 2e-2 * rms, f"mutation {m} not detected"
