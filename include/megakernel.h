@@ -51,6 +51,7 @@ enum MegaStatus : int {
     kErrLaunch = 5,         // hipLaunchKernel failed
     kErrUnsupported = 6,    // option not supported by this build
     kErrDevice = 7,         // read_status: the device status word reports an error
+    kErrScratch = 8,        // mm_launch_full_noalloc: layout larger than its scratch
 };
 
 // Device status words: the workspace region MegaLayout::status, rewritten by
@@ -234,6 +235,18 @@ int mm_launch_l1(const fp8mega::MegaLaunchArgs* a, void* stream);
 int mm_launch_l2(const fp8mega::MegaLaunchArgs* a, void* stream);
 int mm_launch_reduce(const fp8mega::MegaLaunchArgs* a, void* stream);
 int mm_launch_full(const fp8mega::MegaLaunchArgs* a, void* stream);
+// launch_full for callers that cannot allocate (code under graph capture,
+// tight serving loops, harnesses that forbid hipMalloc).  No reference
+// counterpart.  The workspace is a fixed device array inside the library
+// (mm_noalloc_scratch_bytes() bytes, 64 MiB, one per GPU, held until the
+// process ends) instead of a->rwk, which is ignored with workspace_bytes:
+// the layout of a->max_tokens must fit it (kErrScratch otherwise; e.g. up to
+// ~540 tokens at E=256, top-8, H=6144, I=2048).  The caller still passes the
+// inputs and outputs.  The call allocates nothing.  Every call on one GPU
+// shares that array: calls that overlap on one GPU (other streams, other
+// threads) race; skip_prologue reuses the previous call's routing.
+int mm_launch_full_noalloc(const fp8mega::MegaLaunchArgs* a, void* stream);
+long long mm_noalloc_scratch_bytes(void);
 int mm_launch_empty(int grid, int threads, long long smem, void* stream);
 int mm_launch_dispatch(const fp8mega::MegaLaunchArgs* a, uint8_t* pool, void* stream);
 // fp8mega::read_status (synchronises `stream`).

@@ -50,6 +50,7 @@ STATUS_NAMES = {
     0: "ok", 1: "null pointer", 2: "unsupported dims", 3: "workspace too small",
     4: "tokens exceed max_tokens", 5: "kernel launch failed", 6: "unsupported option",
     7: "device status word reports an error",
+    8: "layout larger than the no-alloc scratch",
 }
 ERR_DEVICE = 7
 
@@ -63,6 +64,7 @@ class MegaError(RuntimeError):
 EXPORTS = (
     "mm_abi_version", "mm_args_size", "mm_args_offset", "mm_layout", "mm_launch_prelude",
     "mm_launch_compute", "mm_launch_l1", "mm_launch_l2", "mm_launch_reduce", "mm_launch_full",
+    "mm_launch_full_noalloc", "mm_noalloc_scratch_bytes",
     "mm_launch_empty", "mm_launch_dispatch", "mm_read_status", "mm_fill_weights_lane", "mm_pack_weights",
     "mm_pack_weights_from_reference",
     "mm_fill_weights_normal", "mm_quant_act", "mm_selftest_convert", "mm_dump_kernel_resources",
@@ -90,11 +92,12 @@ def lib():
     L.mm_layout.restype = c_int
     L.mm_layout.argtypes = [c_int] * 6 + [ctypes.POINTER(MegaLayout)]
     for n in ("mm_launch_prelude", "mm_launch_compute", "mm_launch_l1", "mm_launch_l2",
-              "mm_launch_reduce", "mm_launch_full"):
+              "mm_launch_reduce", "mm_launch_full", "mm_launch_full_noalloc"):
         getattr(L, n).restype = c_int
         getattr(L, n).argtypes = [A, c_vp]
     L.mm_launch_dispatch.restype = c_int
     L.mm_launch_dispatch.argtypes = [A, c_vp, c_vp]
+    L.mm_noalloc_scratch_bytes.restype = ctypes.c_longlong
     L.mm_read_status.restype = c_int
     L.mm_read_status.argtypes = [A, c_vp, c_int, c_vp]
     L.mm_launch_empty.restype = c_int

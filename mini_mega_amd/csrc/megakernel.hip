@@ -6,10 +6,11 @@
 // Nothing here allocates or reads the environment, and only read_status
 // synchronises: every launch entry point only validates its arguments and
 // enqueues kernels on `stream`, so the layer is capture-safe.  The workspace
-// is caller-owned.
+// is caller-owned, or (mm_launch_full_noalloc) the file-scope `scratch`.
 #include <cstddef>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "mm_kernels.h"
 
@@ -276,6 +277,61 @@ int do_dispatch(const MegaLaunchArgs& a, uint8_t* pool, hipStream_t s) {
     return launched(kOk);
 }
 
+// ---- the allocation-free entry point's workspace --------------------------
+// One fixed device array per GPU the library runs on, held until the process
+// ends.  Host code never uses its name as an address (on the host it is a
+// stand-in symbol): scratch_on_device() resolves the device address once per
+// device with hipGetSymbolAddress, with that device current.
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, or null (status in *st).
+uint8_t* scratch_on_device(int* st) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *st = kErrLaunch;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+            *st = kErrLaunch;
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
+    }
+    *st = kOk;
+    return g_scratch_ptr[dev];
+}
+
+// launch_full with the workspace taken from `scratch` instead of a.rwk (which
+// is ignored, as is a.workspace_bytes).  The layout of a.max_tokens must fit
+// kScratchBytes (kErrScratch otherwise).  Every region the kernels read is
+// written earlier in the same launch (status, histograms, items, slots, the
+// intermediate rows), so nothing needs clearing between calls; with
+// skip_prologue the routing of the previous call on this device is reused.
+int do_full_noalloc(const MegaLaunchArgs& a, hipStream_t s) {
+    const int st0 = check_dims(a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
+    if (st0 != kOk) return st0;
+    const int st1 = check_capacity(a.max_tokens, a.topk, a.hidden, a.intermediate, a.win_cap);
+    if (st1 != kOk) return st1;
+    const MegaLayout L =
+        layout(a.max_tokens, a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
+    if (L.total > kScratchBytes) return kErrScratch;
+    int st = kOk;
+    uint8_t* ws = scratch_on_device(&st);
+    if (st != kOk) return st;
+    MegaLaunchArgs b = a;
+    b.rwk = reinterpret_cast<rwk_data*>(ws);
+    b.workspace_bytes = kScratchBytes;
+    return do_full(b, s);
+}
+
 int record(int st) {
     g_last_error = st;
     if (st != kOk) std::fprintf(stderr, "[fp8mega] error %d\n", st);
@@ -442,6 +498,8 @@ extern "C" {
 
 int mm_abi_version(void) { return 1; }
 
+long long mm_noalloc_scratch_bytes(void) { return (long long)fp8mega::kScratchBytes; }
+
 size_t mm_args_size(void) { return sizeof(MegaLaunchArgs); }
 
 long long mm_args_offset(const char* f) {
@@ -480,6 +538,7 @@ MM_WRAP(mm_launch_l1, fp8mega::do_l1)
 MM_WRAP(mm_launch_l2, fp8mega::do_l2)
 MM_WRAP(mm_launch_reduce, fp8mega::do_reduce)
 MM_WRAP(mm_launch_full, fp8mega::do_full)
+MM_WRAP(mm_launch_full_noalloc, fp8mega::do_full_noalloc)
 #undef MM_WRAP
 
 int mm_launch_dispatch(const MegaLaunchArgs* a, uint8_t* pool, void* stream) {
