@@ -283,6 +283,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-probes", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--probes-only", action="store_true",
+                    help="only the measured-peak probes (a 2 GiB copy, a 4 GiB read-only "
+                         "stream, MFMA loops): the HBM counter calibration runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the whole layer on ONE GPU (all 256 experts); "
@@ -302,6 +305,9 @@ def main():
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
     L = mm.lib()
+    if args.probes_only:
+        print(json.dumps({"measured_peaks": measured_peaks(torch, L, stream)}), flush=True)
+        return
     _log("setup: weights")
     w = inputs.make_weights_normal(E, H, I, seed=args.seed + 1)
     torch.cuda.synchronize()

@@ -132,14 +132,14 @@ def check_routing(c: Case, r: Run):
     assert np.array_equal(r.perm, perm), "canonical permutation differs"
     assert np.array_equal(r.pair_pos, pair_pos), "pair slots differ"
     assert r.status[0] == 0, f"device status word {r.status[0]}"
-    # work items: each expert's rows split evenly into ceil(count / m_tile) items
+    # work items: each expert's rows split into items of sz rows, the even
+    # share of ceil(count / m_tile) items rounded up to whole 16-row tiles
     m_tile = int(r.buf.layout.m_tile)
     want = []
     for e, cnt in enumerate(counts.tolist()):
         if cnt == 0:
             continue
-        nm = -(-cnt // m_tile)
-        sz = -(-cnt // nm)
+        nm, sz = item_split(cnt, m_tile)
         want += [(e, j * sz, min(cnt, (j + 1) * sz), j | (nm << 16)) for j in range(nm)]
     assert int(r.status[1]) == len(want), "work item count differs"
     got = r.buf.items(len(want)).cpu().numpy() if want else np.zeros((0, 4), np.int32)
@@ -152,15 +152,26 @@ def check_routing(c: Case, r: Run):
             f"XCD unit ranges differ (nb={nb})"
 
 
+def item_split(cnt, m_tile):
+    """(items, rows per item) of an expert with cnt routed rows: the even
+    share of ceil(cnt / m_tile) items rounded up to a multiple of 16 rows;
+    the last item takes the remainder."""
+    if cnt == 0:
+        return 0, 0
+    nm0 = -(-cnt // m_tile)
+    sz = -(-(-(-cnt // nm0)) // 16) * 16
+    return -(-cnt // sz), sz
+
+
 def xcd_cuts(counts, m_tile, nb, max_items):
     """The routing scan's XCD ranges, restated: expert e's nb * nm units (nm
-    items of at most sz rows) each cost max(9, 2 + token tiles of sz); XCD x
+    items of at most sz rows, item_split) each cost max(9, 2 + token tiles
+    of sz); XCD x
     starts where the running cost crosses x/8 of the total, and every range
     is clamped to the grid's share (nb * max_items + 8) // 8."""
     nms, ucs = [], []
     for cnt in np.asarray(counts).tolist():
-        nm = -(-cnt // m_tile)
-        sz = -(-cnt // nm) if nm else 0
+        nm, sz = item_split(cnt, m_tile)
         nms.append(nm)
         ucs.append(max(9, 2 + min((sz + 15) // 16, 16)))
     n = sum(nms)

@@ -235,8 +235,8 @@ SMALL = [
 
 def test_every_token_tile_count():
     """Expert e gets 16(e+1) - 3 rows, so one 256-row window runs each of the
-    big GEMMs' token-tile specialisations (1..8, then 10, 12, 14, 16 for the
-    odd counts above 8) on at least one item; every expert is checked staged."""
+    big GEMMs' token-tile specialisations (1..16) on one item; every expert
+    is checked staged."""
     E, K, H, I = 16, 8, 512, 256
     rows = [16 * (e + 1) - 3 for e in range(E)]
     ids = np.repeat(np.arange(E), rows)
