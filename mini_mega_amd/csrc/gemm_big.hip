@@ -29,7 +29,9 @@
 //   * epilogues as in gemm.hip: L1 SwiGLU + fp8 (raw, or per-128 UE8M0 with
 //     the 128-column amax reduced over the waves in LDS), L2 bf16.
 // Work units are numbered so that each XCD runs a contiguous range of them:
-// the N-blocks of one item share that XCD's L2 for the item's activations.
+// the N-blocks of one item share that XCD's L2 for the item's activations;
+// in L1 the last units of each range go out through a per-XCD ticket queue
+// that a few extra workgroups of the other XCDs also drain.
 #include "mm_kernels.h"
 
 namespace mm {
@@ -305,16 +307,70 @@ struct BigItem {
 // this order runs the n readers of each block on neighbouring CUs of one XCD
 // at the same time, so all but one take the block from that XCD's L2.  (The
 // expert of unit u is the one of item u / nb: its items are consecutive.)
-// The XCDs take workgroups round-robin, so workgroup L (the k-th of XCD L%8,
-// k = L/8) runs unit xcd_cuts[L%8] + k: each XCD walks a contiguous range,
-// the ranges cut by the routing scan at equal modelled cost (skewed routing
-// mixes units of 1 and 16 token tiles).  The grid has nb * max_items + 8
-// workgroups, at least 8 times the longest range; the surplus exits.
-__device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& it) {
+// The routing scan cuts the unit list into one contiguous range per XCD at
+// equal modelled cost, and the XCDs take workgroups round-robin: workgroup L
+// is the k-th of XCD x = L%8, k = L/8 (measured on MI355X with the XCC_ID
+// register: every workgroup ran on XCD L%8).
+// Static bulk, dynamic tail.  While k < (range of x) - kQueueTail, workgroup
+// L runs unit cuts[x] + k, with no atomic on its way to its first load.  The
+// last kQueueTail units of each range go out by ticket from that XCD's
+// counter, to its workgroups k < range; the next kStealers workgroups of the
+// XCD take tickets from the other XCDs' tails, so that an XCD that runs
+// ahead of its modelled cost finishes the others' last units instead of
+// idling.  Every later workgroup exits at once: the grid (nb * max_items +
+// 8) is sized for the largest item count, and a surplus workgroup that paid
+// atomics while holding a CU's LDS delayed the real tail (L2 650 -> 900 us
+// at T = 2048).  The last ticket taker of a launch zeroes the counters for
+// the next one.  Measured on MI355X (time-stamped workgroups): without the
+// queue the XCDs' last L1 units ended up to 55 us apart at T = 512, 175 us
+// at T = 8192 and 120 us with Zipf(1.1) skew; with it 22, 55 and 91 us.  A
+// stolen unit runs without the victim XCD's L2 contents, so the kernel span
+// shrinks less than the spread: L1 with Zipf(1.1) T = 2048 1260 -> 1216 us,
+// T = 8192 -9 us, T = 512 and 2048 even.  L2's units are a third as long,
+// and there the queue cost 6-10 us at T = 512 and 2048, so only L1 uses it
+// (big_unit<true>); L2 runs each range statically.
+__device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool own) {
+    int u = -1;
+    for (int d = own ? 0 : 1; d < 8 && u < 0; ++d) {
+        const int xx = (x + d) & 7;
+        const int lo = p.xcd_cuts[xx], hi = p.xcd_cuts[xx + 1];
+        const int tail = min(hi - lo, kQueueTail);
+        if (tail <= 0) continue;
+        const int t = atomicAdd(&p.queue[xx], 1);
+        if (t < tail) u = hi - tail + t;
+    }
+    // ticket takers of this launch: per XCD, its workgroups from the tail
+    // through its stealers (as many as the grid holds)
+    int takers = 0;
+    for (int xx = 0; xx < 8; ++xx) {
+        const int range = p.xcd_cuts[xx + 1] - p.xcd_cuts[xx];
+        const int wgs = ((int)gridDim.x - xx + 7) >> 3;
+        takers += min(wgs, range + kStealers) - (range - min(range, kQueueTail));
+    }
+    if (atomicAdd(&p.queue[8], 1) == takers - 1) {
+#pragma unroll
+        for (int i = 0; i < kQueueInts; ++i) p.queue[i] = 0;
+    }
+    return u;
+}
+
+template <bool kTailQueue>
+__device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& it, int* s_unit) {
     const int L = blockIdx.x;
     const int x = L & 7, k = L >> 3;
-    const int u = p.xcd_cuts[x] + k;
-    if (u >= p.xcd_cuts[x + 1]) return false;
+    const int lo = p.xcd_cuts[x], hi = p.xcd_cuts[x + 1], range = hi - lo;
+    int u = lo + k;
+    if (!kTailQueue) {
+        if (k >= range) return false;
+    } else if (k >= range + kStealers) {
+        return false;
+    }
+    if (kTailQueue && k >= range - min(range, kQueueTail)) {
+        if (threadIdx.x == 0) *s_unit = claim_tail_unit(p, x, k < range);
+        __syncthreads();
+        u = *s_unit;
+        if (u < 0) return false;
+    }
     const int4* items = reinterpret_cast<const int4*>(p.items);
     const int im = u / nb;                 // item-major item: same expert
     const int jn = items[im].w;
@@ -488,8 +544,9 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
 template <int W>
 __device__ __forceinline__ void l1_big(const GemmParams& p) {
     __shared__ BigSmem sm;
+    __shared__ int s_unit;
     BigItem it;
-    if (!big_unit(p, p.I / kL1BlockH, it)) return;
+    if (!big_unit<true>(p, p.I / kL1BlockH, it, &s_unit)) return;
     const int KT = p.H >> 7, I = p.I, G = p.G;
     const int tiles = (it.rows + 15) >> 4;
     // scales: x rows through perm[]; W1 tiles as l1_tile_row places them
@@ -548,8 +605,9 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
 template <int W>
 __device__ __forceinline__ void l2_big(const GemmParams& p) {
     __shared__ BigSmem sm;
+    __shared__ int s_unit;
     BigItem it;
-    if (!big_unit(p, p.H / kL2BlockN, it)) return;
+    if (!big_unit<false>(p, p.H / kL2BlockN, it, &s_unit)) return;
     const int KT = p.I >> 7, H = p.H;
     const int tiles = (it.rows + 15) >> 4;
     // scales: ffn rows in slot order; W2 tiles of this block's 256 channels

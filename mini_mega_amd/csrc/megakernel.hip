@@ -207,6 +207,7 @@ int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     p.out8 = b.ws + b.L.ffn;
     p.out_sf = b.ws + b.L.ffn_sf;
     p.xcd_cuts = p.status + mm::kCutsL1;
+    p.queue = at<int>(b, b.L.status) + mm::kQueueL1;
     const int nb = a.intermediate / mm::kL1BlockH;
     launch_gemm(kL1Small, mm::l1_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
@@ -224,6 +225,7 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     p.w_sf = a.w2_sf;
     p.out16 = at<uint16_t>(b, b.L.l2);
     p.xcd_cuts = p.status + mm::kCutsL2;
+    p.queue = at<int>(b, b.L.status) + mm::kQueueL2;
     const int nb = a.hidden / mm::kL2BlockN;
     launch_gemm(kL2Small, mm::l2_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);

@@ -32,6 +32,15 @@ constexpr int kStatusInts = 64;     // workspace status words
 constexpr int kStatusItemOverflow = fp8mega::kStatusItemOverflow;
 constexpr int kCutsL1 = 16;         // status[16..24]: XCD unit ranges of the L1 big GEMM
 constexpr int kCutsL2 = 32;         // status[32..40]: the same for L2
+// Tail queues of the big GEMMs: per XCD a ticket counter over the last
+// kQueueTail units of its range, plus a count of the workgroups that took
+// tickets (status[44..52] for L1, [53..61] for L2; zeroed by the routing
+// scan and again by the last ticket taker of each launch).
+constexpr int kQueueInts = 9;
+constexpr int kQueueL1 = 44;
+constexpr int kQueueL2 = kQueueL1 + kQueueInts;
+constexpr int kQueueTail = 32;      // units per XCD handed out by ticket (one per CU)
+constexpr int kStealers = 8;        // workgroups per XCD past its range that take others' tickets
 
 // Parameters of the two grouped GEMMs (one struct so that the launcher and
 // the kernels agree on one argument list).
@@ -46,6 +55,7 @@ struct GemmParams {
                               // (item j of the expert's n)
     const int* status;        // [1] = number of items
     const int* xcd_cuts;      // [9]: XCD x runs big-GEMM units [cuts[x], cuts[x+1])
+    int* queue;               // [kQueueInts]: the tail queue of these units
     const uint32_t* perm;     // slot -> pair (L1 gathers x rows through it)
     uint8_t* out8;            // L1: ffn fp8 [P][I]
     uint8_t* out_sf;          // L1: ffn scales [P][I/128] (ffn_ue8m0)

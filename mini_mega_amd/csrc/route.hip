@@ -148,6 +148,7 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
             reinterpret_cast<int4*>(items)[it] = make_int4(e, m0, min(cnt, m0 + sz), j | (nm << 16));
         }
     }
+    if (threadIdx.x < 2 * kQueueInts) status[kQueueL1 + threadIdx.x] = 0;   // tail queues
     if (threadIdx.x == 0) {
         status[1] = min(nitems, max_items);
         status[2] = slots;

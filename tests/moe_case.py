@@ -144,6 +144,9 @@ def check_routing(c: Case, r: Run):
     assert int(r.status[1]) == len(want), "work item count differs"
     got = r.buf.items(len(want)).cpu().numpy() if want else np.zeros((0, 4), np.int32)
     assert np.array_equal(got, np.array(want, dtype=np.int32).reshape(-1, 4)), "work items differ"
+    # the big GEMMs' tail queues (status[44..61]) are zero again after the
+    # launch: their last ticket takers reset them (the routing scan also does)
+    assert not np.any(r.status[44:62]), f"tail queues not reset: {r.status[44:62]}"
     # XCD unit ranges of the big GEMMs (status[16..24] for L1, [32..40] for L2)
     max_items = int(r.buf.layout.max_items)
     for base, nb in ((16, c.I // 128), (32, c.H // 256)):
