@@ -127,18 +127,17 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     const int off = block_exclusive_scan(cnt, smem, &slots);
     if (e < E) offsets[e] = off;
     if (threadIdx.x == 0) offsets[E] = slots;
-    // Work items: the expert's rows split into items of sz rows, sz the even
-    // share of ceil(cnt / m_tile) items rounded up to whole 16-row token
-    // tiles (the last item takes the remainder), so that only an expert's
-    // last item has a partial tile and no item re-streams the expert's
-    // weights for a small remainder.  Measured on MI355X at T = 8192: the
-    // even split (rows rounded up to even token tiles) ran 11.7% more
-    // token-tile MFMA work than the routed rows need, this split 2.9%.
-    // Record: (expert, first row, end row, index within the expert | item
-    // count of the expert << 16).
-    const int nm0 = (cnt + m_tile - 1) / m_tile;
-    const int sz = nm0 > 0 ? (((cnt + nm0 - 1) / nm0 + 15) & ~15) : 0;
-    const int nm = nm0 > 0 ? (cnt + sz - 1) / sz : 0;
+    // Work items: the expert's rows split evenly into ceil(cnt / m_tile)
+    // items of at most m_tile rows (no item re-streams the expert's weights
+    // for a small remainder).  The items of one expert then have equal token
+    // tile counts, so the units that read one weight block run in lockstep
+    // and all but the first take it from L2.  (Measured on MI355X at T =
+    // 8192: splitting at 16-row multiples instead ran 2% less MFMA work but
+    // its unequal items drifted apart; L1 fetched 9.30 vs 7.33 GB and the
+    // layer took 4908-4943 vs 4841-4854 us.)  Record: (expert, first row,
+    // end row, index within the expert | item count of the expert << 16).
+    const int nm = (cnt + m_tile - 1) / m_tile;
+    const int sz = nm > 0 ? (cnt + nm - 1) / nm : 0;
     int nitems = 0;
     const int ioff = block_exclusive_scan(nm, smem, &nitems);
     for (int j = 0; j < nm; ++j) {

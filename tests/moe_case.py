@@ -132,8 +132,7 @@ def check_routing(c: Case, r: Run):
     assert np.array_equal(r.perm, perm), "canonical permutation differs"
     assert np.array_equal(r.pair_pos, pair_pos), "pair slots differ"
     assert r.status[0] == 0, f"device status word {r.status[0]}"
-    # work items: each expert's rows split into items of sz rows, the even
-    # share of ceil(count / m_tile) items rounded up to whole 16-row tiles
+    # work items: each expert's rows split evenly into ceil(count / m_tile) items
     m_tile = int(r.buf.layout.m_tile)
     want = []
     for e, cnt in enumerate(counts.tolist()):
@@ -156,14 +155,12 @@ def check_routing(c: Case, r: Run):
 
 
 def item_split(cnt, m_tile):
-    """(items, rows per item) of an expert with cnt routed rows: the even
-    share of ceil(cnt / m_tile) items rounded up to a multiple of 16 rows;
-    the last item takes the remainder."""
+    """(items, rows per item) of an expert with cnt routed rows: ceil(cnt /
+    m_tile) items of an even share each; the last takes the remainder."""
     if cnt == 0:
         return 0, 0
-    nm0 = -(-cnt // m_tile)
-    sz = -(-(-(-cnt // nm0)) // 16) * 16
-    return -(-cnt // sz), sz
+    nm = -(-cnt // m_tile)
+    return nm, -(-cnt // nm)
 
 
 def xcd_cuts(counts, m_tile, nb, max_items):
