@@ -275,6 +275,15 @@ void mm_dump_kernel_resources(void);
 // 16x16x128 fp8 MFMA, mode 1 on the bf16 MFMA after the exact conversion.
 int mm_probe_mfma_dot(const uint8_t* a, const uint8_t* b, int K, int N, int mode, float* out,
                       void* stream);
+// The layer's L2 recomputed over routed slots, out[s][n] fp32 ([P][H]):
+// groups holds ngroups int4 {expert, first slot, end slot, 0} of at most 16
+// slots each; ffn [P][I] + ffn_sf [P][I/128] as L1 writes them, w2 logical
+// row-major [E][H][I] + w2_sf [E][H/128][I/128].  mode 0: the 16x16x128 fp8
+// MFMA with the UE8M0 bytes as its scale operands; mode 1: the bf16 MFMA
+// after the exact conversion, in the L2 GEMM's operand roles and k order.
+int mm_probe_l2_rows(const uint8_t* ffn, const uint8_t* ffn_sf, const uint8_t* w2,
+                     const uint8_t* w2_sf, const int* groups, int ngroups, int H, int I, int mode,
+                     float* out, void* stream);
 // Reads `bytes` (a multiple of 16) once with non-temporal 16-byte loads;
 // sink holds grid * 256 words.
 int mm_probe_stream_read(const uint8_t* src, unsigned long long bytes, uint32_t* sink,

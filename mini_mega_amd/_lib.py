@@ -68,7 +68,7 @@ EXPORTS = (
     "mm_launch_empty", "mm_launch_dispatch", "mm_read_status", "mm_fill_weights_lane", "mm_pack_weights",
     "mm_pack_weights_from_reference",
     "mm_fill_weights_normal", "mm_quant_act", "mm_selftest_convert", "mm_dump_kernel_resources",
-    "mm_probe_mfma_dot", "mm_probe_stream_read", "mm_probe_mfma_rate",
+    "mm_probe_mfma_dot", "mm_probe_l2_rows", "mm_probe_stream_read", "mm_probe_mfma_rate",
 )
 
 _lib = None
@@ -118,6 +118,8 @@ def lib():
     L.mm_dump_kernel_resources.restype = None
     L.mm_probe_mfma_dot.restype = c_int
     L.mm_probe_mfma_dot.argtypes = [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_vp]
+    L.mm_probe_l2_rows.restype = c_int
+    L.mm_probe_l2_rows.argtypes = [c_vp] * 5 + [c_int] * 4 + [c_vp, c_vp]
     L.mm_probe_stream_read.restype = c_int
     L.mm_probe_stream_read.argtypes = [c_vp, ctypes.c_ulonglong, c_vp, c_int, c_vp]
     L.mm_probe_mfma_rate.restype = c_int

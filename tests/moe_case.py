@@ -63,6 +63,19 @@ class Case:
         return None if self.s2 is None else np.ascontiguousarray(self.s2[e].cpu().numpy())
 
 
+def logical_weights(c: Case):
+    """All experts' weights unpacked to logical row-major numpy ([E][2I][H] and
+    [E][H][I]; about 9.7 GB at full size)."""
+    w1 = np.empty((c.E, 2 * c.I, c.H), np.uint8)
+    w2 = np.empty((c.E, c.H, c.I), np.uint8)
+    a1 = c.w1.view(torch.uint8).cpu().numpy()
+    a2 = c.w2.view(torch.uint8).cpu().numpy()
+    for e in range(c.E):
+        w1[e] = inputs.unpack_tiles(a1[e].ravel(), 2 * c.I, c.H)
+        w2[e] = inputs.unpack_tiles(a2[e].ravel(), c.H, c.I)
+    return w1, w2
+
+
 def normal_case(E, K, H, I, T, seed, scaled=True, zipf=None, win=0, idx=None, wts=None):
     _, xq, xsf = inputs.make_x(T, H, seed=seed, scaled=scaled)
     (w1, s1), (w2, s2) = inputs.make_weights_normal(E, H, I, seed=seed + 100)

@@ -11,7 +11,6 @@ import pytest
 import torch
 
 import mini_mega_amd as mm
-from mini_mega_amd import inputs
 from oracle import oracle as orc
 
 import moe_case as mc
@@ -34,18 +33,6 @@ def _gpu():
     yield
 
 
-def _logical_weights(c):
-    """All experts' weights unpacked to logical row-major numpy (about 9.7 GB)."""
-    w1 = np.empty((E, 2 * I, H), np.uint8)
-    w2 = np.empty((E, H, I), np.uint8)
-    a1 = c.w1.view(torch.uint8).cpu().numpy()
-    a2 = c.w2.view(torch.uint8).cpu().numpy()
-    for e in range(E):
-        w1[e] = inputs.unpack_tiles(a1[e].ravel(), 2 * I, H)
-        w2[e] = inputs.unpack_tiles(a2[e].ravel(), H, I)
-    return w1, w2
-
-
 @pytest.mark.parametrize("T,zipf,ntok", [(512, None, None), (2048, None, None),
                                          (2048, 1.1, None), (8192, None, 1024)])
 def test_full_output_end_to_end(T, zipf, ntok):
@@ -54,7 +41,7 @@ def test_full_output_end_to_end(T, zipf, ntok):
     c = mc.normal_case(E, K, H, I, T, seed=T + 1, scaled=True, zipf=zipf)
     r = mc.run_layer(c)
     mc.check_routing(c, r)
-    w1, w2 = _logical_weights(c)
+    w1, w2 = mc.logical_weights(c)
     s1 = np.ascontiguousarray(c.s1.cpu().numpy())
     s2 = np.ascontiguousarray(c.s2.cpu().numpy())
     tok = np.arange(ntok or T)
