@@ -172,7 +172,8 @@ def cpu_baseline(x, xsf, idx, wts, w1, s1, w2, s2, counts, T):
 
 def measured_peaks(torch, L, stream):
     """The box's own rates: a 2 GiB device copy (torch), a 4 GiB read-only
-    non-temporal stream and dense MFMA issue loops (library probes)."""
+    non-temporal stream (the better of two grids) and dense MFMA issue loops
+    (library probes)."""
     sp = stream.cuda_stream
     out = {}
     n = 2 << 30
@@ -183,15 +184,17 @@ def measured_peaks(torch, L, stream):
     out["copy_GBs"] = round(2 * n / (ms * 1e-3) / 1e9, 1)
     del dst
     big = torch.empty(4 << 30, dtype=torch.uint8, device="cuda").fill_(3)
-    grid = 256 * 16
-    sink = torch.empty(grid * 256, dtype=torch.int32, device="cuda")
+    sink = torch.empty(1024 * 256, dtype=torch.int32, device="cuda")
+    best = 0.0
+    for grid in (512, 1024):   # two and four workgroups of 4 waves per CU
 
-    def rd():
-        rc = L.mm_probe_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(), grid, sp)
-        assert rc == 0
-    rd()
-    ms = time_events(rd, 5, stream)
-    out["read_GBs"] = round(big.numel() / (ms * 1e-3) / 1e9, 1)
+        def rd():
+            rc = L.mm_probe_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(), grid, sp)
+            assert rc == 0
+        rd()
+        ms = time_events(rd, 5, stream)
+        best = max(best, big.numel() / (ms * 1e-3) / 1e9)
+    out["read_GBs"] = round(best, 1)
     del big, src, sink
     fs = torch.empty(4096 * 4, dtype=torch.float32, device="cuda")
     for mode, name, flop in ((0, "bf16", 16 * 16 * 32 * 2), (1, "fp8", 16 * 16 * 128 * 2)):

@@ -284,8 +284,9 @@ int mm_probe_mfma_dot(const uint8_t* a, const uint8_t* b, int K, int N, int mode
 int mm_probe_l2_rows(const uint8_t* ffn, const uint8_t* ffn_sf, const uint8_t* w2,
                      const uint8_t* w2_sf, const int* groups, int ngroups, int H, int I, int mode,
                      float* out, void* stream);
-// Reads `bytes` (a multiple of 16) once with non-temporal 16-byte loads;
-// sink holds grid * 256 words.
+// Reads `bytes` once with non-temporal 16-byte loads, each of the grid
+// workgroups (256 threads) one contiguous bytes / grid chunk; bytes must be a
+// multiple of grid * 32 KiB.  sink holds grid * 256 words.
 int mm_probe_stream_read(const uint8_t* src, unsigned long long bytes, uint32_t* sink,
                          int grid, void* stream);
 // grid workgroups of 4 waves, each running iters x 8 independent MFMAs
