@@ -155,6 +155,14 @@ constexpr int big_stages() {
 template <int W, int NT>
 constexpr int big_read_ahead() { return (W == 8 && NT > 12) ? 2 : 3; }
 
+// Bodies of at most this many token tiles issue their first weight stages
+// before the unit's scale staging, whose load round trip then overlaps the
+// weights' HBM latency.  Measured on MI355X against issuing them after it:
+// T = 512 layer 1515-1517 vs 1521 us (L2 537 vs 541-545 us); with the bound
+// at 8 tiles, T = 2048 L1 took 1153-1155 vs 1146-1147 us, so larger bodies
+// keep the later issue (at NT = 16 the early stages also made the body spill).
+constexpr int kEarlyMaxTiles = 2;
+
 // One k-step, software-pipelined by hand.  The step's 4*NT chunks (k-group
 // q, token tile j) each hold: the LDS read of the activation operand D
 // chunks ahead, a share of the conversions of the next k-group's weight
@@ -265,23 +273,30 @@ __device__ __forceinline__ void big_tail(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& s
 // double buffer fed from XS register stages.  Weights: S register stages.
 // Whole groups of S k-steps run without any branch; a remainder (only when
 // KT is not a multiple of S) runs through the guarded tail.
-template <int W, int NT, int S>
+// The first S - 1 weight stages of a unit.
+template <int WT, int S>
+__device__ __forceinline__ void w_prologue(WStage<WT> (&w)[S], const WTiles<WT>& wt, int KT) {
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) w_load<WT>(w[s], wt, min(s, KT - 1));
+}
+
+// kEarly: the caller issued the first weight stages (w_prologue) before the
+// unit's scale staging, so that their HBM latency overlaps it.
+template <int W, int NT, int S, bool kEarly>
 __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                              XLoader<W, NT>& xl, const WTiles<Geo<W>::kWT>& wt,
-                                             int KT) {
+                                             int KT, WStage<Geo<W>::kWT> (&w)[S]) {
     constexpr int kWT = Geo<W>::kWT;
     constexpr int XS = XLoader<W, NT>::XS;
     static_assert(XS == 1 || S % 2 == 0, "two activation stages alternate within a group");
     static_assert(S >= 2 && S <= 8, "stages");
-    WStage<kWT> w[S];
 #pragma unroll
     for (int t = 0; t < kWT; ++t)
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
     xl.issue(0, 0);
     if constexpr (XS == 2) xl.issue(min(1, KT - 1), 1);
-#pragma unroll
-    for (int s = 0; s < S - 1; ++s) w_load<kWT>(w[s], wt, min(s, KT - 1));
+    if constexpr (!kEarly) w_prologue<kWT, S>(w, wt, KT);
     xl.commit(sm, 0, 0, 0);
     __syncthreads();
     v8bf a0[kWT];
@@ -458,24 +473,30 @@ __device__ __forceinline__ int l1_tile_row(int bx, int bt, int G) {
     return (hw / G) * 2 * G + (hw % G) + (up ? G : 0);
 }
 
-template <int W, int NT>
-__device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm) {
+template <int W, int NT, class ScalesF>
+__device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
+                                            ScalesF stage_scales) {
     constexpr int kWT = Geo<W>::kWT, kH = kWT / 2;
+    constexpr int S = big_stages<W, NT, false>();
+    constexpr bool kEarly = NT <= kEarlyMaxTiles;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, G = p.G, KT = H >> 7;
+    const uint8_t* we = p.w + (size_t)it.e * (size_t)(2 * I) * H;
+    WTiles<kWT> wt;
+    wt.KT = KT;
+#pragma unroll
+    for (int t = 0; t < kWT; ++t) wt.set(t, we, l1_tile_row<W>(it.bx, kWT * wave + t, G) >> 4, lane);
+    WStage<kWT> w[S];
+    if constexpr (kEarly) w_prologue<kWT, S>(w, wt, KT);
+    stage_scales();
     XLoader<W, NT> xl;
     xl.base = p.x;
     big_loader_init<W, NT>(xl, [&](int r) {
         const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
         return (p.perm[slot] / (uint32_t)p.topk) * (uint32_t)H;
     });
-    const uint8_t* we = p.w + (size_t)it.e * (size_t)(2 * I) * H;
-    WTiles<kWT> wt;
-    wt.KT = KT;
-#pragma unroll
-    for (int t = 0; t < kWT; ++t) wt.set(t, we, l1_tile_row<W>(it.bx, kWT * wave + t, G) >> 4, lane);
     v4f acc[kWT][NT];
-    big_mainloop<W, NT, big_stages<W, NT, false>()>(acc, sm, xl, wt, KT);
+    big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
 
     // h = silu(g) * u: hidden column hw + 16c + 4*(L/16) + i, token 16*j + L%16
     const int hw = it.bx * kL1BlockH + wave * (kL1BlockH / W);
@@ -550,17 +571,19 @@ __device__ __forceinline__ void l1_big(const GemmParams& p) {
     const int KT = p.H >> 7, I = p.I, G = p.G;
     const int tiles = (it.rows + 15) >> 4;
     // scales: x rows through perm[]; W1 tiles as l1_tile_row places them
-    big_load_scales<W>(
-        sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
-        [&](int r) {
-            const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
-            return p.x_sf + (size_t)(p.perm[slot] / (uint32_t)p.topk) * KT;
-        },
-        [&](int t) {
-            const int rho = l1_tile_row<W>(it.bx, t, G);
-            return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
-        });
-#define MM_L1_BODY(n) l1_big_body<W, n>(p, it, sm)
+    auto stage_scales = [&]() {
+        big_load_scales<W>(
+            sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
+            [&](int r) {
+                const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
+                return p.x_sf + (size_t)(p.perm[slot] / (uint32_t)p.topk) * KT;
+            },
+            [&](int t) {
+                const int rho = l1_tile_row<W>(it.bx, t, G);
+                return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
+            });
+    };
+#define MM_L1_BODY(n) l1_big_body<W, n>(p, it, sm, stage_scales)
     MM_BIG_DISPATCH(MM_L1_BODY)
 #undef MM_L1_BODY
 }
@@ -568,24 +591,30 @@ __device__ __forceinline__ void l1_big(const GemmParams& p) {
 __global__ void __launch_bounds__(512) l1_big_kernel(GemmParams p) { l1_big<8>(p); }
 
 // ---------------------------------------------------------------------- L2 --
-template <int W, int NT>
-__device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm) {
+template <int W, int NT, class ScalesF>
+__device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
+                                            ScalesF stage_scales) {
     constexpr int kWT = Geo<W>::kWT;
+    constexpr int S = big_stages<W, NT, true>();
+    constexpr bool kEarly = NT <= kEarlyMaxTiles;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, KT = I >> 7;
-    XLoader<W, NT> xl;
-    xl.base = p.x;
-    big_loader_init<W, NT>(xl, [&](int r) {
-        return (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
-    });
     const int n0 = it.bx * kL2BlockN + wave * (kL2BlockN / W);   // the wave's output channels
     const uint8_t* we = p.w + (size_t)it.e * (size_t)H * I;
     WTiles<kWT> wt;
     wt.KT = KT;
 #pragma unroll
     for (int t = 0; t < kWT; ++t) wt.set(t, we, (n0 >> 4) + t, lane);
+    WStage<kWT> w[S];
+    if constexpr (kEarly) w_prologue<kWT, S>(w, wt, KT);
+    stage_scales();
+    XLoader<W, NT> xl;
+    xl.base = p.x;
+    big_loader_init<W, NT>(xl, [&](int r) {
+        return (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
+    });
     v4f acc[kWT][NT];
-    big_mainloop<W, NT, big_stages<W, NT, true>()>(acc, sm, xl, wt, KT);
+    big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         const int r = 16 * j + (lane & 15);
@@ -611,14 +640,16 @@ __device__ __forceinline__ void l2_big(const GemmParams& p) {
     const int KT = p.I >> 7, H = p.H;
     const int tiles = (it.rows + 15) >> 4;
     // scales: ffn rows in slot order; W2 tiles of this block's 256 channels
-    big_load_scales<W>(
-        sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
-        [&](int r) { return p.x_sf + (size_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * KT; },
-        [&](int t) {
-            const int n = it.bx * kL2BlockN + t * 16;
-            return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
-        });
-#define MM_L2_BODY(n) l2_big_body<W, n>(p, it, sm)
+    auto stage_scales = [&]() {
+        big_load_scales<W>(
+            sm, KT, min(tiles * 16, kBigRows), p.x_sf != nullptr, p.w_sf != nullptr,
+            [&](int r) { return p.x_sf + (size_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * KT; },
+            [&](int t) {
+                const int n = it.bx * kL2BlockN + t * 16;
+                return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
+            });
+    };
+#define MM_L2_BODY(n) l2_big_body<W, n>(p, it, sm, stage_scales)
     MM_BIG_DISPATCH(MM_L2_BODY)
 #undef MM_L2_BODY
 }
