@@ -11,7 +11,9 @@ top-k combine).  `value` is the headline layer's algorithmic HBM throughput
 (GB/s): bytes = sum over active experts of (3*H*I + scale bytes) + T*H +
 T*H/128 + 12*T*k + 2*T*H, divided by the measured step time.  The other
 configs are reported under "configs", each with its layer time, TFLOP/s,
-HBM and MFMA fractions and per-kernel times; "measured_peaks" holds the
+HBM and MFMA fractions and per-kernel times, and the layer time under the
+reference's own protocol (a HIP graph of 10 launches, best of 5 replays:
+graph_us_per_layer_min5); "measured_peaks" holds the
 box's own HBM and MFMA rates from the library's probes, beside the
 datasheet peaks the fractions use.
 
@@ -211,6 +213,30 @@ def measured_peaks(torch, L, stream):
     return out
 
 
+def graph_min5(torch, mm, L, a, n=10):
+    """The reference's timing protocol (docs/02_测试流程与性能标准.md:13-36):
+    n identical layer launches captured in one HIP graph, 2 warm-up replays,
+    then the best of 5 timed replays; returns ms per layer."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(n):
+                rc = L.mm_launch_full(ctypes.byref(a), s.cuda_stream)
+                if rc:
+                    raise mm.MegaError("mm_launch_full", rc)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    best = min(time_events(g.replay, 1, cur) for _ in range(5))
+    del g
+    return best / n
+
+
 def run_config(torch, mm, inputs, L, stream, w, T, zipf, seed, steps, warmup, kernel_iters):
     """One workload: fresh inputs and buffer, warmup, `steps` timed layers,
     then each stage timed alone (the routing stays valid in the workspace)."""
@@ -246,6 +272,7 @@ def run_config(torch, mm, inputs, L, stream, w, T, zipf, seed, steps, warmup, ke
         stage[name] = time_events(lambda fn=fn: fn(ctypes.byref(a), sp), kernel_iters, stream)
     step()
     torch.cuda.synchronize()
+    graph_ms = graph_min5(torch, mm, L, a)
     P = int(counts.sum())
     lb = layer_bytes(counts, T)
     fl = layer_flops(P)
@@ -255,6 +282,7 @@ def run_config(torch, mm, inputs, L, stream, w, T, zipf, seed, steps, warmup, ke
     l2_tf = 2.0 * H * I * P / (stage["l2"] * 1e-3) / 1e12
     res = {
         "layer_us": round(ms * 1e3, 1), "wall_us_per_step": round(wall_ms * 1e3, 1),
+        "graph_us_per_layer_min5": round(graph_ms * 1e3, 1),
         "hbm_GBs": round(lb / (ms * 1e-3) / 1e9, 1),
         "hbm_frac": round(lb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "tflops": round(tflops, 1),
