@@ -332,15 +332,18 @@ def test_single_token_then_empty_batch():
 
 
 # -------------------------------------------------- check.cu-identical inputs --
-def test_checkcu_inputs_full_size_t512():
-    """check.cu's own inputs at R=32, TPR=16 (T=512) remapped to one GPU:
+@pytest.mark.parametrize("tpr", [1, 4, 16, 32, 33, 64, 128, 256, 512])
+def test_checkcu_inputs_full_size(tpr):
+    """check.cu's own inputs at R=32 and every TPR of its balanced plan
+    (kBalancedTprs, test/check.cu:49: T = 32 .. 16384) remapped to one GPU:
     routing exact, every ffn byte saturated to 0x7E (closed form), L2 and
     REDUCE at check.cu tolerances."""
-    _say("check.cu inputs T=512 full size")
-    c = mc.checkcu_case(32, 16)
+    _say(f"check.cu inputs TPR={tpr} (T={32 * tpr}) full size")
+    c = mc.checkcu_case(32, tpr)
     r = mc.run_layer(c)
     mc.check_routing(c, r)
     slots = int(r.offsets[-1])
+    assert slots == 32 * tpr * 8
     ffn = r.buf.ffn(slots).cpu().numpy()
     assert np.all(ffn == 0x7E)
     for e in (0, 7, 255):
