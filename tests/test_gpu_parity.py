@@ -332,10 +332,11 @@ def test_single_token_then_empty_batch():
 
 
 # -------------------------------------------------- check.cu-identical inputs --
-@pytest.mark.parametrize("tpr", [1, 4, 16, 32, 33, 64, 128, 256, 512])
+@pytest.mark.parametrize("tpr", [1, 4, 16, 24, 32, 33, 64, 128, 256, 512])
 def test_checkcu_inputs_full_size(tpr):
-    """check.cu's own inputs at R=32 and every TPR of its balanced plan
-    (kBalancedTprs, test/check.cu:49: T = 32 .. 16384) remapped to one GPU:
+    """check.cu's own inputs at R=32 and every TPR of its balanced plans
+    (kBalancedTprs, test/check.cu:49, and the smoke plan's 24, :922: T = 32
+    .. 16384) remapped to one GPU:
     routing exact, every ffn byte saturated to 0x7E (closed form), L2 and
     REDUCE at check.cu tolerances."""
     _say(f"check.cu inputs TPR={tpr} (T={32 * tpr}) full size")
@@ -349,6 +350,50 @@ def test_checkcu_inputs_full_size(tpr):
     for e in (0, 7, 255):
         mc.check_l2(c, r, e)
     mc.check_reduce(c, r)
+
+
+@pytest.mark.parametrize("launch", [804900, 809200])
+def test_checkcu_tk_fixed_routes_full_layer(launch):
+    """The reference smoke plan's recorded routes (TK_INFO launches 804900 and
+    809200, its case0 / case2: test/check.cu:44-48,905-925) with check.cu's
+    inputs at full size on one GPU: routing exact, every ffn byte saturated,
+    L2 staged on the busiest and the lightest expert, REDUCE bit-exact, and a
+    graph of three launches replayed bit-identical to the eager output (the
+    plan's eager + graph x N pair)."""
+    from test_oracle import _tk_launches
+    per_expert = _tk_launches()[launch]
+    tpr = int(per_expert.sum()) // (32 * 8)
+    _say(f"check.cu inputs on TK launch {launch} (T={32 * tpr})")
+    idx = orc.routes_from_counts(per_expert, 32, 8, tpr, 8)
+    c = mc.checkcu_case(32, tpr, idx=idx)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    assert np.array_equal(r.counts, per_expert)
+    slots = int(r.offsets[-1])
+    assert np.all(r.buf.ffn(slots).cpu().numpy() == 0x7E)
+    nz = np.nonzero(r.counts)[0]
+    order = nz[np.argsort(r.counts[nz], kind="stable")]
+    for e in {int(order[-1]), int(order[0])}:
+        mc.check_l2(c, r, e)
+    mc.check_reduce(c, r)
+    ys = [torch.empty((c.T, c.H), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for y in ys:
+                mm.fp8_mega_moe(y, c.w1, c.w2, r.buf)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(2):
+        for y in ys:
+            y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for y in ys:
+            assert np.array_equal(y.float().cpu().numpy(), r.y), f"replay {rep} differs"
 
 
 # ------------------------------------------------------------ full sizes --
