@@ -396,6 +396,35 @@ def test_checkcu_tk_fixed_routes_full_layer(launch):
             assert np.array_equal(y.float().cpu().numpy(), r.y), f"replay {rep} differs"
 
 
+@pytest.mark.parametrize("launch", [45400, 84900, 151000])
+def test_real_decode_routes_full_layer(launch):
+    """Routes of the reference's real GLM-5.2 decode corpus (test/76.real_decode/
+    dataset.tk_info: the most skewed launch, a median one and the smallest)
+    through the full-size layer with BASELINE's scaled inputs: routing exact,
+    staged L1/L2 on the busiest, a median and the lightest active expert,
+    REDUCE bit-exact, and the whole chain on a token subset."""
+    from test_oracle import _tk_launches
+    per_expert = _tk_launches("tk_real_decode.log")[launch]
+    tpr = int(per_expert.sum()) // (32 * 8)
+    T = 32 * tpr
+    _say(f"real decode launch {launch} (T={T}, busiest expert {int(per_expert.max())} rows)")
+    idx = orc.routes_from_counts(per_expert, 32, 8, tpr, 8)
+    _, wts = inputs.route(T, 256, 8, seed=launch)
+    c = mc.normal_case(256, 8, 6144, 2048, T, seed=launch % 1000 + 5, scaled=True, idx=idx,
+                       wts=wts)
+    r = mc.run_layer(c)
+    mc.check_routing(c, r)
+    assert np.array_equal(r.counts, per_expert)
+    nz = np.nonzero(r.counts)[0]
+    order = nz[np.argsort(r.counts[nz], kind="stable")]
+    for e in {int(order[-1]), int(order[len(order) // 2]), int(order[0])}:
+        mc.check_l1(c, r, e, max_rows=48)
+        mc.check_l2(c, r, e, max_rows=48)
+    mc.check_reduce(c, r)
+    err, rms, cos = mc.check_e2e_tokens(c, r, [0, T // 3, T - 1])
+    _say(f"  subset e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
+
+
 # ------------------------------------------------------------ full sizes --
 @pytest.mark.parametrize("T,zipf", [(512, None), (2048, None), (2048, 1.1), (8192, None)])
 def test_full_size_layer(T, zipf):

@@ -125,13 +125,17 @@ def test_route_matches_bruteforce(T, K, E, cap):
     assert np.array_equal(pair_pos, bpos)
 
 
-def _tk_launches():
+def _tk_launches(name="tk_info_anchors.log"):
+    """Per-expert counts [256] of each TK_INFO launch in a committed fixture
+    (32 ranks x 8 local experts)."""
     import os
     import re
-    path = os.path.join(os.path.dirname(__file__), "golden", "tk_info_anchors.log")
+    path = os.path.join(os.path.dirname(__file__), "golden", name)
     data = {}
     for line in open(path):
         m = re.search(r"\[TK_INFO\] rank=(\d+) launch=(\d+) n=8 : (.*)", line)
+        if m is None:
+            continue
         data.setdefault(int(m.group(2)), {})[int(m.group(1))] = list(map(int, m.group(3).split()))
     out = {}
     for launch, ranks in data.items():
@@ -153,6 +157,21 @@ def test_tk_fixture_routes_reproduce_counts(launch):
     assert np.array_equal(counts, per_expert)
     for row in idx:
         assert len(set(row.tolist())) == 8  # duplicate free per token
+
+
+@pytest.mark.parametrize("launch", [45400, 84900, 151000])
+def test_real_decode_fixture_routes_reproduce_counts(launch):
+    """The same for launches of the reference's real GLM-5.2 decode corpus
+    (test/76.real_decode/dataset.tk_info; committed excerpt): the most skewed
+    launch puts 398 of 4096 pairs on one expert and leaves 140 experts empty."""
+    per_expert = _tk_launches("tk_real_decode.log")[launch]
+    total = int(per_expert.sum())
+    assert total % (32 * 8) == 0
+    idx = orc.routes_from_counts(per_expert, 32, 8, total // (32 * 8), 8)
+    counts, *_ = orc.route(idx, 256)
+    assert np.array_equal(counts, per_expert)
+    for row in idx:
+        assert len(set(row.tolist())) == 8
 
 
 def test_balanced_routes_exactly_16_per_expert():
