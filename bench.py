@@ -302,6 +302,49 @@ def run_config(torch, mm, inputs, L, stream, w, T, zipf, seed, steps, warmup, ke
     return res, inputs_for_cpu
 
 
+def run_tk_info(torch, mm, inputs, L, stream, w, path, steps, warmup, seed, max_launches):
+    """The reference bench's --tk-info mode (test/mybench.cu): every launch of
+    a TK_INFO routing log whose routed pairs split into whole top-8 tokens,
+    replayed through the layer with this benchmark's inputs; mean / median /
+    p90 / max layer time over the launches."""
+    (w1, s1), (w2, s2) = w
+    launches = inputs.read_tk_info(path)
+    keep = [(l, pe) for l, pe in sorted(launches.items())
+            if pe.size == E and int(pe.sum()) % K == 0 and int(pe.sum()) > 0
+            and pe.max() <= int(pe.sum()) // K]
+    if max_launches:
+        keep = keep[:max_launches]
+    Tmax = max(int(pe.sum()) // K for _, pe in keep)
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, Tmax, K, H, I)
+    y = torch.empty((Tmax, H), dtype=torch.bfloat16, device="cuda")
+    sp = stream.cuda_stream
+    times = {}
+    for i, (launch, pe) in enumerate(keep):
+        T = int(pe.sum()) // K
+        idx = inputs.routes_with_counts(pe, K)
+        _, wts = inputs.route(T, E, K, seed=seed + i)
+        _, xq, xsf = inputs.make_x(T, H, seed=seed + i, scaled=True)
+        buf.x.view(torch.uint8)[:T].copy_(xq)
+        buf.x_sf[:T].copy_(xsf)
+        buf.topk_idx[:T].copy_(torch.from_numpy(idx))
+        buf.topk_weights[:T].copy_(torch.from_numpy(wts))
+        a = buf.make_args(T, (w1, s1), (w2, s2), y_bf16=y)
+
+        def step():
+            rc = L.mm_launch_full(ctypes.byref(a), sp)
+            if rc:
+                raise mm.MegaError("mm_launch_full", rc)
+        for _ in range(warmup):
+            step()
+        times[launch] = time_events(step, steps, stream) * 1e3
+    buf.destroy()
+    v = np.array(list(times.values()))
+    return {"file": path, "launches": len(times), "tokens_max": Tmax,
+            "mean_us": round(float(v.mean()), 1), "median_us": round(float(np.median(v)), 1),
+            "p90_us": round(float(np.percentile(v, 90)), 1), "max_us": round(float(v.max()), 1),
+            "layer_us": {str(k): round(t, 1) for k, t in times.items()}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -314,6 +357,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-probes", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--tk-info", default=None,
+                    help="also replay every launch of a TK_INFO routing log (the reference "
+                         "bench's --tk-info), e.g. tests/golden/tk_real_decode.log")
+    ap.add_argument("--tk-max", type=int, default=0, help="at most this many --tk-info launches")
     ap.add_argument("--probes-only", action="store_true",
                     help="only the measured-peak probes (a 2 GiB copy, a 4 GiB read-only "
                          "stream, MFMA loops): the HBM counter calibration runs")
@@ -398,6 +445,10 @@ def main():
             "frac_of_fp8_peak": round(r["l1"]["TFLOPs"] / FP8_PEAK_TFLOPS, 4),
             "layer_frac_of_fp8_peak": r["fp8_mfma_frac"],
             "note": "the GEMMs run on the bf16 MFMA (exact fp8 -> bf16 operands)"}
+    if args.tk_info:
+        _log(f"tk_info replay of {args.tk_info}")
+        out["tk_info"] = run_tk_info(torch, mm, inputs, L, stream, w, args.tk_info, 10, 2,
+                                     args.seed + 500, args.tk_max)
     if not args.no_probes:
         _log("measured peaks")
         out["measured_peaks"] = measured_peaks(torch, L, stream)

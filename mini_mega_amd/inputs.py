@@ -61,6 +61,43 @@ def route(T: int, E: int, topk: int, seed: int, zipf_s: float | None = None,
     return idx.astype(np.int64), w.astype(np.float32)
 
 
+def routes_with_counts(per_expert, topk: int) -> np.ndarray:
+    """topk_idx int64 [T, topk] whose per-expert counts are exactly
+    per_expert (T = sum / topk): every token takes the topk experts with the
+    most rows left (ties to the lower index), so each token's experts are
+    distinct as long as no expert holds more than T rows.  Used to replay a
+    logged routing distribution (the reference bench's --tk-info inputs,
+    test/mybench.cu), not to model any router."""
+    left = np.asarray(per_expert, dtype=np.int64).copy()
+    total = int(left.sum())
+    if total % topk:
+        raise ValueError(f"{total} routed pairs are not a multiple of top-{topk}")
+    T = total // topk
+    if left.max(initial=0) > T:
+        raise ValueError("an expert holds more rows than there are tokens")
+    idx = np.empty((T, topk), np.int64)
+    for t in range(T):
+        pick = np.argsort(-left, kind="stable")[:topk]
+        idx[t] = pick
+        left[pick] -= 1
+    if left.min(initial=0) < 0:
+        raise ValueError("counts cannot be split into distinct top-k rows")
+    return idx
+
+
+def read_tk_info(path: str) -> dict:
+    """{launch: per-expert counts [ranks * experts per rank]} from a TK_INFO
+    log ("[TK_INFO] rank=R launch=L n=N : c0 c1 ..."), the reference's
+    routing-distribution format (test/mega_common.cuh:460-482)."""
+    import re
+    data: dict = {}
+    for line in open(path, encoding="utf-8"):
+        m = re.search(r"\[TK_INFO\] rank=(\d+) launch=(\d+) n=\d+ : (.*)", line)
+        if m:
+            data.setdefault(int(m.group(2)), {})[int(m.group(1))] = [int(v) for v in m.group(3).split()]
+    return {l: np.array([c for r in sorted(rk) for c in rk[r]], np.int64) for l, rk in data.items()}
+
+
 def make_x(T: int, H: int, seed: int, scaled: bool = True):
     """bf16 N(0,1) activations on the device -> (x_bf16, x_fp8 [T,H] uint8,
     x_sf [T,H/128] uint8 or None)."""

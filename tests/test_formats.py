@@ -3,6 +3,7 @@ layout (as transform_weights_from_reference reads it) and the checkpoint
 scale-folding recipe.  The GPU side of the converter is tested in
 test_gpu_parity.py against the plain packer."""
 import numpy as np
+import pytest
 import torch
 
 import mini_mega_amd as mm
@@ -59,3 +60,23 @@ def test_fold_checkpoint_block_scales_recipe():
     assert torch.equal(w13_b[0, 128:, :128].view(torch.uint8), half.view(torch.uint8))
     assert torch.equal(w13_b.view(torch.uint8)[0, 128:, 128:], w13.view(torch.uint8)[0, 128:, 128:])
     assert torch.equal(w13_b.view(torch.uint8)[0, :128], w13.view(torch.uint8)[0, :128])
+
+
+def test_routes_with_counts_reproduce_logged_counts():
+    """inputs.routes_with_counts (the bench's TK_INFO replay) gives exactly the
+    logged per-expert counts with distinct experts per token, on every launch
+    of both committed TK_INFO fixtures, and rejects counts that cannot form
+    distinct top-k rows."""
+    import os
+    from mini_mega_amd import inputs
+    for name in ("tk_info_anchors.log", "tk_real_decode.log"):
+        launches = inputs.read_tk_info(os.path.join(os.path.dirname(__file__), "golden", name))
+        assert launches
+        for pe in launches.values():
+            idx = inputs.routes_with_counts(pe, 8)
+            assert np.array_equal(np.bincount(idx.ravel(), minlength=pe.size), pe)
+            assert all(len(set(r.tolist())) == 8 for r in idx)
+    with pytest.raises(ValueError):
+        inputs.routes_with_counts(np.array([3, 1]), 2)    # 2 tokens, one expert with 3 rows
+    with pytest.raises(ValueError):
+        inputs.routes_with_counts(np.array([2, 1]), 2)    # 3 pairs: not whole top-2 tokens
