@@ -237,13 +237,15 @@ def graph_min5(torch, mm, L, a, n=10):
     return best / n
 
 
-def run_config(torch, mm, inputs, L, stream, w, T, zipf, seed, steps, warmup, kernel_iters):
+def run_config(torch, mm, inputs, L, stream, w, T, zipf, seed, steps, warmup, kernel_iters,
+               fuse=False):
     """One workload: fresh inputs and buffer, warmup, `steps` timed layers,
     then each stage timed alone (the routing stays valid in the workspace)."""
     (w1, s1), (w2, s2) = w
     _, xq, xsf = inputs.make_x(T, H, seed=seed, scaled=True)
     idx, wts = inputs.route(T, E, K, seed=seed + 2, zipf_s=zipf)
     buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I)
+    buf.fuse_l1l2 = fuse
     buf.x.view(torch.uint8)[:T].copy_(xq)
     buf.x_sf[:T].copy_(xsf)
     buf.topk_idx[:T].copy_(torch.from_numpy(idx))
@@ -361,6 +363,8 @@ def main():
                     help="also replay every launch of a TK_INFO routing log (the reference "
                          "bench's --tk-info), e.g. tests/golden/tk_real_decode.log")
     ap.add_argument("--tk-max", type=int, default=0, help="at most this many --tk-info launches")
+    ap.add_argument("--fuse-l1l2", action="store_true",
+                    help="time the layer with L1 and L2 in one launch (MegaLaunchArgs::fuse_l1l2)")
     ap.add_argument("--probes-only", action="store_true",
                     help="only the measured-peak probes (a 2 GiB copy, a 4 GiB read-only "
                          "stream, MFMA loops): the HBM counter calibration runs")
@@ -395,7 +399,7 @@ def main():
         T, zipf = CONFIGS[n]
         _log(f"config T={T} zipf={zipf}: {args.warmup} warmup + {args.steps} timed steps")
         res, ci = run_config(torch, mm, inputs, L, stream, w, T, zipf, args.seed + 10 * i,
-                             args.steps, args.warmup, args.kernel_iters)
+                             args.steps, args.warmup, args.kernel_iters, fuse=args.fuse_l1l2)
         res["workload"] = f"T={T}" + (f" zipf({zipf})" if zipf else " balanced")
         results[n] = res
         if i == 0:
@@ -424,7 +428,8 @@ def main():
         "config": {"workload": f"fused fp8 MoE layer E=256 top-8 H=6144 I=2048 "
                                f"{head['workload']}",
                    "tokens": T0, "experts": E, "topk": K, "hidden": H, "intermediate": I,
-                   "scales": "UE8M0 (x per-token per-128, W 128x128, ffn per-128)"},
+                   "scales": "UE8M0 (x per-token per-128, W 128x128, ffn per-128)",
+                   "l1_l2": "one fused launch" if args.fuse_l1l2 else "two launches"},
         "layer_us": head["layer_us"],
         "layer_tflops": head["tflops"],
         "layer_hbm_frac": head["hbm_frac"],

@@ -59,7 +59,8 @@ enum MegaStatus : int {
 // without skip_prologue) and readable after it with read_status():
 //   [0]  error bits (kStatusItemOverflow: the work-item table overflowed; the
 //        GEMMs then skip the experts past it -- the layout's bound makes this
-//        unreachable, the bit guards the kernels' assumption)
+//        unreachable, the bit guards the kernels' assumption; kStatusWaitTimeout:
+//        with fuse_l1l2, an L2 unit stopped waiting after max_spins polls)
 //   [1]  work items, [2] routed slots,
 //   [3]  pairs dropped by slot_capacity,
 //   [4]  pairs whose expert id is outside [0, num_experts) (dropped)
@@ -68,6 +69,7 @@ enum MegaStatus : int {
 // are void and its host CHECKs exit (src/host_layout.cuh:18-26).
 enum MegaDeviceStatus : int {
     kStatusItemOverflow = 1,
+    kStatusWaitTimeout = 2,   // fuse_l1l2: an L2 unit gave up waiting for its item's L1 units
 };
 
 // One launch's host arguments (reference: src/megakernel.h:54-114; fields
@@ -100,7 +102,8 @@ struct MegaLaunchArgs {
     float* y = nullptr;                    // [tokens][H] fp32 (may be null if y_bf16)
 
     // [4] tuning
-    int max_spins = 0;                     // unused (no cross-rank waits on one GPU)
+    int max_spins = 0;                     // fuse_l1l2: polls per L1 -> L2 wait (0: ~1 s);
+                                           // no cross-rank waits on one GPU
     int skip_prologue = 0;                 // >0: reuse routing of the previous launch
 
     // [5] debug: none
@@ -120,6 +123,11 @@ struct MegaLaunchArgs {
     int ffn_ue8m0 = 0;                     // L1 output requant: per-128 UE8M0 (1) or raw (0);
                                            // must be 1 exactly when scales are given
     uint16_t* y_bf16 = nullptr;            // [tokens][H] bf16 (may be null if y)
+    int fuse_l1l2 = 0;                     // 1: L1 and L2 in one launch, L2 units starting on
+                                           // an item once its L1 units are done (per-item
+                                           // ready counters; reference src/compute_big.cuh:
+                                           // 1948-1997).  Windows > 32 rows; max_spins > 0
+                                           // bounds each wait (else ~1 s).
 };
 
 // Byte offsets of every region inside the workspace (the single-GPU
@@ -131,7 +139,8 @@ struct MegaLayout {
     int64_t chunk_hist;    // int32[nchunks][E] per-chunk histograms -> prefixes
     int64_t counts;        // int32[E]   per-expert routed rows (after cap)
     int64_t offsets;       // int32[E+1] exclusive prefix of counts
-    int64_t items;         // int32[max_items][4] (expert, first row, end row, j | n << 16) work items
+    int64_t items;         // int32[max_items][4] (expert, first row, end row, j | n << 16) work
+                           // items, then int32[max_items] per-item L1 ready counters (fuse_l1l2)
     int64_t perm;          // uint32[P]  pair index per slot (canonical order)
     int64_t pair_pos;      // int32[P]   slot per pair or -1
     int64_t xq;            // uint8[max_tokens][H]     folded fp8 x (in_bf16)

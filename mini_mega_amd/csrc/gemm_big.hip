@@ -72,7 +72,7 @@ struct alignas(16) BigSmem {
 // flight while kt+1 is written to LDS; with one (above 12 token tiles, where
 // registers go to accumulators, and a k-step's 4*NT MFMA groups alone cover
 // an L2 hit; measured even with two at T = 8192), kt+1 is loaded during kt.
-template <int W, int NT>
+template <int W, int NT, int kAux = 0>
 struct XLoader {
     static constexpr int kThreads = Geo<W>::kThreads;
     static constexpr int U = (NT * 128 + kThreads - 1) / kThreads;
@@ -93,7 +93,7 @@ struct XLoader {
 
     __device__ __forceinline__ void issue(int kt, int rs) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) reg[rs][u] = load16_rows(base, off[u], kt * kTileK);
+        for (int u = 0; u < U; ++u) reg[rs][u] = load16_rows<kAux>(base, off[u], kt * kTileK);
     }
     // Writes chunk u of register stage rs, scaled by 2^(e - 127), to LDS stage xw.
     __device__ __forceinline__ void commit_chunk(uint8_t* xw, int rs, int u, uint32_t e) {
@@ -182,13 +182,13 @@ constexpr int kEarlyMaxTiles = 2;
 // compiler's wait counts stay partial).  After: the barrier that publishes
 // the committed activations.  a0 carries the converted k-group-0 operand from
 // one step to the next.
-template <int W, int NT, int S, int s>
+template <int W, int NT, int S, int s, class XL>
 __device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
-                                         XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
+                                         XL& xl, WStage<Geo<W>::kWT> (&w)[S],
                                          const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
                                          int kt, int KT) {
     constexpr int kWT = Geo<W>::kWT;
-    constexpr int XS = XLoader<W, NT>::XS, U = XLoader<W, NT>::U;
+    constexpr int XS = XL::XS, U = XL::U;
     constexpr int G = 4 * NT, D = big_read_ahead<W, NT>() < G ? big_read_ahead<W, NT>() : G;
     constexpr int rs = XS == 2 ? ((s + 1) & 1) : 0;   // register stage holding k-step kt+1
     const int lane = threadIdx.x & 63;
@@ -204,7 +204,7 @@ __device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& s
     uint32_t xs[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
-        xs[u] = sm.sfx[XLoader<W, NT>::row_of(XLoader<W, NT>::chunk(u))][kn];
+        xs[u] = sm.sfx[XL::row_of(xl.chunk(u))][kn];
     // LDS bases of this step's read and write buffers.  Opaque to the
     // optimiser: otherwise it hoists every operand address of the unrolled
     // group out of the loop into a register of its own (the buffer parity of
@@ -254,9 +254,9 @@ __device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& s
     __syncthreads();
 }
 
-template <int W, int NT, int S, int s>
+template <int W, int NT, int S, int s, class XL>
 __device__ __forceinline__ void big_group(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
-                                          XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
+                                          XL& xl, WStage<Geo<W>::kWT> (&w)[S],
                                           const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
                                           int kb, int KT) {
     big_step<W, NT, S, s>(acc, sm, xl, w, wt, a0, kb + s, KT);
@@ -264,9 +264,9 @@ __device__ __forceinline__ void big_group(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& 
 }
 
 // The KT % S remaining k-steps, one guarded step each.
-template <int W, int NT, int S, int r>
+template <int W, int NT, int S, int r, class XL>
 __device__ __forceinline__ void big_tail(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
-                                         XLoader<W, NT>& xl, WStage<Geo<W>::kWT> (&w)[S],
+                                         XL& xl, WStage<Geo<W>::kWT> (&w)[S],
                                          const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
                                          int KF, int KT) {
     if (KF + r < KT) {
@@ -288,12 +288,12 @@ __device__ __forceinline__ void w_prologue(WStage<WT> (&w)[S], const WTiles<WT>&
 
 // kEarly: the caller issued the first weight stages (w_prologue) before the
 // unit's scale staging, so that their HBM latency overlaps it.
-template <int W, int NT, int S, bool kEarly>
+template <int W, int NT, int S, bool kEarly, class XL>
 __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
-                                             XLoader<W, NT>& xl, const WTiles<Geo<W>::kWT>& wt,
+                                             XL& xl, const WTiles<Geo<W>::kWT>& wt,
                                              int KT, WStage<Geo<W>::kWT> (&w)[S]) {
     constexpr int kWT = Geo<W>::kWT;
-    constexpr int XS = XLoader<W, NT>::XS;
+    constexpr int XS = XL::XS;
     static_assert(XS == 1 || S % 2 == 0, "two activation stages alternate within a group");
     static_assert(S >= 2 && S <= 8, "stages");
 #pragma unroll
@@ -319,7 +319,7 @@ __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSme
 
 // Per-unit context shared by the two kernels.
 struct BigItem {
-    int e, m0, rows, off, bx;
+    int e, m0, rows, off, bx, item;
 };
 
 // Work units: an expert with n items has n * nb units, numbered from
@@ -350,7 +350,7 @@ struct BigItem {
 // T = 8192 -9 us, T = 512 and 2048 even.  L2's units are a third as long,
 // and there the queue cost 6-10 us at T = 512 and 2048, so only L1 uses it
 // (big_unit<true>); L2 runs each range statically.
-__device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool own) {
+__device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool own, int grid) {
     int u = -1;
     for (int d = own ? 0 : 1; d < 8 && u < 0; ++d) {
         const int xx = (x + d) & 7;
@@ -365,7 +365,7 @@ __device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool 
     int takers = 0;
     for (int xx = 0; xx < 8; ++xx) {
         const int range = p.xcd_cuts[xx + 1] - p.xcd_cuts[xx];
-        const int wgs = ((int)gridDim.x - xx + 7) >> 3;
+        const int wgs = (grid - xx + 7) >> 3;
         takers += min(wgs, range + kStealers) - (range - min(range, kQueueTail));
     }
     if (atomicAdd(&p.queue[8], 1) == takers - 1) {
@@ -375,9 +375,10 @@ __device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool 
     return u;
 }
 
+// Workgroup L of a grid of `grid` (the big GEMM's own share of the launch).
 template <bool kTailQueue>
-__device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& it, int* s_unit) {
-    const int L = blockIdx.x;
+__device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& it, int* s_unit,
+                                         int L, int grid) {
     const int x = L & 7, k = L >> 3;
     const int lo = p.xcd_cuts[x], hi = p.xcd_cuts[x + 1], range = hi - lo;
     int u = lo + k;
@@ -387,7 +388,7 @@ __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& i
         return false;
     }
     if (kTailQueue && k >= range - min(range, kQueueTail)) {
-        if (threadIdx.x == 0) *s_unit = claim_tail_unit(p, x, k < range);
+        if (threadIdx.x == 0) *s_unit = claim_tail_unit(p, x, k < range, grid);
         __syncthreads();
         u = *s_unit;
         if (u < 0) return false;
@@ -398,7 +399,8 @@ __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& i
     const int i0 = im - (jn & 0xffff), n = jn >> 16;
     const int local = u - nb * i0;
     it.bx = local / n;
-    const int4 v = items[i0 + local % n];
+    it.item = i0 + local % n;
+    const int4 v = items[it.item];
     it.e = v.x;
     it.m0 = v.y;
     it.rows = v.z - v.y;
@@ -416,7 +418,9 @@ __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& i
 // time.  Measured on MI355X against byte-wise staging into [k-step][row]:
 // L1 T = 512 944-945 vs 948 us, T = 2048 1133-1135 vs 1144-1151, T = 8192
 // 2910-2928 vs 2936-2961; layer -0.3 to -0.8%.
-template <int W, class RowF, class TileF>
+// kCoherent: the row scales were written by another XCD during this launch
+// (the fused L1 -> L2 handoff) and are read at device scope.
+template <int W, bool kCoherent = false, class RowF, class TileF>
 __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, bool has_w,
                                                 RowF row_scale, TileF tile_scale) {
     constexpr int T = Geo<W>::kThreads;
@@ -425,9 +429,13 @@ __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, 
         uint8_t* dst = &sm.sfx[r][0];
         if (src && (KT & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
             for (int k = 0; k < KT; k += 16)
-                *reinterpret_cast<v4i*>(dst + k) = load16(src + k);
+                *reinterpret_cast<v4i*>(dst + k) =
+                    kCoherent ? load16_rows<kBufferSc1>(src, 0, k) : load16(src + k);
         } else if (src) {
-            for (int k = 0; k < KT; ++k) dst[k] = src[k];
+            for (int k = 0; k < KT; ++k)
+                dst[k] = kCoherent ? __hip_atomic_load(src + k, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : src[k];
         } else {
             for (int k = 0; k < KT; k += 4) *reinterpret_cast<uint32_t*>(dst + k) = 0x7f7f7f7fu;
         }
@@ -465,9 +473,8 @@ __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, 
 
 // Sets the loader's row offsets: row r of the item (r >= rows: row 0,
 // whose bytes are loaded but whose results are never stored).
-template <int W, int NT, class RowOff>
-__device__ __forceinline__ void big_loader_init(XLoader<W, NT>& xl, RowOff row_off) {
-    using XL = XLoader<W, NT>;
+template <class XL, class RowOff>
+__device__ __forceinline__ void big_loader_init(XL& xl, RowOff row_off) {
 #pragma unroll
     for (int u = 0; u < XL::U; ++u) {
         const int i = XL::chunk(u);
@@ -490,10 +497,22 @@ __device__ __forceinline__ int l1_tile_row(int bx, int bt, int G) {
     return (hw / G) * 2 * G + (hw % G) + (up ? G : 0);
 }
 
-template <int W, int NT, class ScalesF>
+// kFused: the L2 units of the same launch read this item's ffn rows (the
+// fused L1 -> L2 handoff).  The rows and scales are then written with
+// device-scope relaxed stores (write-through: no L2 write-back release is
+// needed), every wave waits for its stores, and one thread bumps the item's
+// ready counter after the workgroup barrier.
+template <int W, int NT, bool kFused, class ScalesF>
 __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
                                             ScalesF stage_scales) {
     constexpr int kWT = Geo<W>::kWT, kH = kWT / 2;
+    auto put4 = [](uint8_t* dst, uint32_t v) {
+        if constexpr (kFused)
+            __hip_atomic_store(reinterpret_cast<uint32_t*>(dst), v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        else
+            *reinterpret_cast<uint32_t*>(dst) = v;
+    };
     constexpr int S = big_stages<W, NT, false>();
     constexpr bool kEarly = NT <= kEarlyMaxTiles;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -508,7 +527,7 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
     stage_scales();
     XLoader<W, NT> xl;
     xl.base = p.x;
-    big_loader_init<W, NT>(xl, [&](int r) { return sm.tok[r] * (uint32_t)H; });
+    big_loader_init(xl, [&](int r) { return sm.tok[r] * (uint32_t)H; });
     v4f acc[kWT][NT];
     big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
 
@@ -553,10 +572,16 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
                 const size_t slot = (size_t)(it.off + it.m0 + r);
 #pragma unroll
                 for (int c = 0; c < kH; ++c)
-                    *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4)) =
-                        pack4_fp8(hv[c][j][0] * inv, hv[c][j][1] * inv, hv[c][j][2] * inv,
-                                  hv[c][j][3] * inv);
-                if (wave == 0 && lane < 16) p.out_sf[slot * I128 + it.bx] = (uint8_t)sb;
+                    put4(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4),
+                         pack4_fp8(hv[c][j][0] * inv, hv[c][j][1] * inv, hv[c][j][2] * inv,
+                                   hv[c][j][3] * inv));
+                if (wave == 0 && lane < 16) {
+                    if constexpr (kFused)
+                        __hip_atomic_store(p.out_sf + slot * I128 + it.bx, (uint8_t)sb,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else
+                        p.out_sf[slot * I128 + it.bx] = (uint8_t)sb;
+                }
             }
         }
     } else {
@@ -567,21 +592,28 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
                 const size_t slot = (size_t)(it.off + it.m0 + r);
 #pragma unroll
                 for (int c = 0; c < kH; ++c)
-                    *reinterpret_cast<uint32_t*>(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4)) =
-                        pack4_fp8(hv[c][j][0], hv[c][j][1], hv[c][j][2], hv[c][j][3]);
+                    put4(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4),
+                         pack4_fp8(hv[c][j][0], hv[c][j][1], hv[c][j][2], hv[c][j][3]));
             }
         }
+    }
+    if constexpr (kFused) {
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's stores are complete at device scope
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(p.ready + it.item, 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
 // NT (the item's token tiles) is uniform over the block, so every wave runs
 // the same body and the same barriers.
-template <int W>
-__device__ __forceinline__ void l1_big(const GemmParams& p) {
-    __shared__ BigSmem sm;
-    __shared__ int s_unit;
+// Workgroup L of the `grid` L1 workgroups.
+template <int W, bool kFused>
+__device__ __forceinline__ void l1_big(const GemmParams& p, BigSmem& sm, int* s_unit, int L,
+                                       int grid) {
     BigItem it;
-    if (!big_unit<true>(p, p.I / kL1BlockH, it, &s_unit)) return;
+    if (!big_unit<true>(p, p.I / kL1BlockH, it, s_unit, L, grid)) return;
     const int KT = p.H >> 7, I = p.I, G = p.G;
     const int tiles = (it.rows + 15) >> 4;
     // scales: x rows through perm[] (each row's token kept in LDS for the
@@ -600,15 +632,21 @@ __device__ __forceinline__ void l1_big(const GemmParams& p) {
                 return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
             });
     };
-#define MM_L1_BODY(n) l1_big_body<W, n>(p, it, sm, stage_scales)
+#define MM_L1_BODY(n) l1_big_body<W, n, kFused>(p, it, sm, stage_scales)
     MM_BIG_DISPATCH(MM_L1_BODY)
 #undef MM_L1_BODY
 }
 
-__global__ void __launch_bounds__(512) l1_big_kernel(GemmParams p) { l1_big<8>(p); }
+__global__ void __launch_bounds__(512) l1_big_kernel(GemmParams p) {
+    __shared__ BigSmem sm;
+    __shared__ int s_unit;
+    l1_big<8, false>(p, sm, &s_unit, blockIdx.x, gridDim.x);
+}
 
 // ---------------------------------------------------------------------- L2 --
-template <int W, int NT, class ScalesF>
+// kFused: the item's ffn rows come from L1 units of the same launch, read at
+// device scope (the caller's stage_scales waits for them first).
+template <int W, int NT, bool kFused, class ScalesF>
 __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
                                             ScalesF stage_scales) {
     constexpr int kWT = Geo<W>::kWT;
@@ -625,9 +663,9 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     WStage<kWT> w[S];
     if constexpr (kEarly) w_prologue<kWT, S>(w, wt, KT);
     stage_scales();
-    XLoader<W, NT> xl;
+    XLoader<W, NT, kFused ? kBufferSc1 : 0> xl;
     xl.base = p.x;
-    big_loader_init<W, NT>(xl, [&](int r) {
+    big_loader_init(xl, [&](int r) {
         return (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
     });
     v4f acc[kWT][NT];
@@ -648,17 +686,34 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     }
 }
 
-template <int W>
-__device__ __forceinline__ void l2_big(const GemmParams& p) {
-    __shared__ BigSmem sm;
-    __shared__ int s_unit;
+// Workgroup L of the `grid` L2 workgroups.  kFused: before reading the
+// item's ffn rows, wait until its ready counter reaches p.ready_target (the
+// L1 blocks of an item), polling with a sleep; after p.spin_limit polls the
+// workgroup gives up, sets kStatusWaitTimeout in the status word and goes on
+// (the output is then wrong and the status says so; the kernel never hangs).
+template <int W, bool kFused>
+__device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_unit, int L,
+                                       int grid) {
     BigItem it;
-    if (!big_unit<false>(p, p.H / kL2BlockN, it, &s_unit)) return;
+    if (!big_unit<false>(p, p.H / kL2BlockN, it, s_unit, L, grid)) return;
     const int KT = p.I >> 7, H = p.H;
     const int tiles = (it.rows + 15) >> 4;
     // scales: ffn rows in slot order; W2 tiles of this block's 256 channels
     auto stage_scales = [&]() {
-        big_load_scales<W>(
+        if constexpr (kFused) {
+            if (threadIdx.x == 0) {
+                for (int n = 0; __hip_atomic_load(p.ready + it.item, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT) < p.ready_target;) {
+                    if (++n >= p.spin_limit) {
+                        atomicOr(p.err, kStatusWaitTimeout);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(8);
+                }
+            }
+            __syncthreads();
+        }
+        big_load_scales<W, kFused>(
             sm, KT, min(tiles * 16, kBigRows), p.w_sf != nullptr,
             [&](int r) -> const uint8_t* {
                 return p.x_sf ? p.x_sf + (size_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * KT
@@ -669,12 +724,30 @@ __device__ __forceinline__ void l2_big(const GemmParams& p) {
                 return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
             });
     };
-#define MM_L2_BODY(n) l2_big_body<W, n>(p, it, sm, stage_scales)
+#define MM_L2_BODY(n) l2_big_body<W, n, kFused>(p, it, sm, stage_scales)
     MM_BIG_DISPATCH(MM_L2_BODY)
 #undef MM_L2_BODY
 }
 
-__global__ void __launch_bounds__(512) l2_big_kernel(GemmParams p) { l2_big<8>(p); }
+__global__ void __launch_bounds__(512) l2_big_kernel(GemmParams p) {
+    __shared__ BigSmem sm;
+    __shared__ int s_unit;
+    l2_big<8, false>(p, sm, &s_unit, blockIdx.x, gridDim.x);
+}
+
+// L1 and L2 in one launch: workgroups [0, g1) run L1 units, the rest L2
+// units, which start on an item as soon as its L1 units are done (g1 is a
+// multiple of 8, so both keep the workgroup -> XCD mapping L % 8).  Each
+// XCD's dispatcher starts all its L1 workgroups before any of its L2
+// workgroups, and no L1 unit waits for anything, so every wait ends.
+__global__ void __launch_bounds__(512) gemm_fused_kernel(GemmParams p1, GemmParams p2, int g1) {
+    __shared__ BigSmem sm;
+    __shared__ int s_unit;
+    if ((int)blockIdx.x < g1)
+        l1_big<8, true>(p1, sm, &s_unit, blockIdx.x, g1);
+    else
+        l2_big<8, true>(p2, sm, &s_unit, (int)blockIdx.x - g1, (int)gridDim.x - g1);
+}
 
 #undef MM_BIG_DISPATCH
 

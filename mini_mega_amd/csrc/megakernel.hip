@@ -246,6 +246,50 @@ int do_reduce(const MegaLaunchArgs& a, hipStream_t s) {
     return launched(kOk);
 }
 
+// L1 and L2 as one launch (fuse_l1l2): gemm_fused_kernel's first g1
+// workgroups run the L1 units, the rest the L2 units, each L2 unit waiting on
+// its item's ready counter (zeroed by the routing scan, or here when the
+// routing is reused).
+int do_l1_l2_fused(const MegaLaunchArgs& a, hipStream_t s) {
+    Bound b;
+    int st = bind(a, b, true);
+    if (st != kOk) return st;
+    if (a.tokens == 0) return kOk;
+    int* ready = at<int>(b, b.L.items) + 4 * b.L.max_items;
+    if (a.skip_prologue) {
+        const int n = b.L.max_items;
+        hipLaunchKernelGGL(mm::fill_int_kernel, dim3((n + 255) / 256), dim3(256), 0, s, ready, n,
+                           0);
+    }
+    const int nb1 = a.intermediate / mm::kL1BlockH, nb2 = a.hidden / mm::kL2BlockN;
+    mm::GemmParams p1 = gemm_params(a, b), p2 = gemm_params(a, b);
+    p1.x = b.x;
+    p1.x_sf = b.x_sf;
+    p1.w = a.w1;
+    p1.w_sf = a.w1_sf;
+    p1.out8 = b.ws + b.L.ffn;
+    p1.out_sf = b.ws + b.L.ffn_sf;
+    p1.xcd_cuts = p1.status + mm::kCutsL1;
+    p1.queue = at<int>(b, b.L.status) + mm::kQueueL1;
+    p2.x = b.ws + b.L.ffn;
+    p2.x_sf = a.ffn_ue8m0 ? b.ws + b.L.ffn_sf : nullptr;
+    p2.w = a.w2;
+    p2.w_sf = a.w2_sf;
+    p2.out16 = at<uint16_t>(b, b.L.l2);
+    p2.xcd_cuts = p2.status + mm::kCutsL2;
+    p2.queue = at<int>(b, b.L.status) + mm::kQueueL2;
+    for (mm::GemmParams* q : {&p1, &p2}) {
+        q->ready = ready;
+        q->ready_target = nb1;
+        q->spin_limit = a.max_spins > 0 ? a.max_spins : mm::kReadySpinLimit;
+        q->err = at<int>(b, b.L.status);
+    }
+    const int g1 = (nb1 * b.L.max_items + 8 + 7) & ~7, g2 = nb2 * b.L.max_items + 8;
+    hipLaunchKernelGGL(mm::gemm_fused_kernel, dim3(g1 + g2), dim3(mm::kBigThreads), 0, s, p1, p2,
+                       g1);
+    return launched(kOk);
+}
+
 int do_compute(const MegaLaunchArgs& a, hipStream_t s) {
     int st = kOk;
     if (!a.skip_prologue) {
@@ -255,6 +299,11 @@ int do_compute(const MegaLaunchArgs& a, hipStream_t s) {
         Bound b;
         st = bind(a, b, false);
         if (st == kOk) fold_x(a, b, s);
+    }
+    if (a.fuse_l1l2 && st == kOk) {
+        Bound b;
+        st = bind(a, b, true);
+        if (st == kOk && b.m_tile > 32) return do_l1_l2_fused(a, s);
     }
     if (st == kOk) st = do_l1(a, s);
     if (st == kOk) st = do_l2(a, s);
@@ -366,7 +415,7 @@ MegaLayout layout(int max_tokens, int topk, int num_experts, int hidden, int int
     L.chunk_hist = o;  o = align256(o + (int64_t)L.nchunks * E * 4);
     L.counts = o;      o = align256(o + E * 4);
     L.offsets = o;     o = align256(o + (E + 1) * 4);
-    L.items = o;       o = align256(o + (int64_t)L.max_items * 16);
+    L.items = o;       o = align256(o + (int64_t)L.max_items * 20);   // + ready counters
     L.perm = o;        o = align256(o + P * 4);
     L.pair_pos = o;    o = align256(o + P * 4);
     L.xq = o;          o = align256(o + (int64_t)max_tokens * hidden);
@@ -472,6 +521,7 @@ void dump_kernel_resources() {
     print_attr("l2_kernel<1>", (const void*)mm::l2_kernel<1>);
     print_attr("l2_kernel<2>", (const void*)mm::l2_kernel<2>);
     print_attr("l2_big_kernel", (const void*)mm::l2_big_kernel);
+    print_attr("gemm_fused_kernel", (const void*)mm::gemm_fused_kernel);
     print_attr("combine", (const void*)mm::combine_kernel);
     std::fflush(stdout);
 }
@@ -498,7 +548,7 @@ using fp8mega::MegaLaunchArgs;
 
 extern "C" {
 
-int mm_abi_version(void) { return 1; }
+int mm_abi_version(void) { return 2; }
 
 long long mm_noalloc_scratch_bytes(void) { return (long long)fp8mega::kScratchBytes; }
 
@@ -514,6 +564,7 @@ long long mm_args_offset(const char* f) {
     MM_FIELD(max_spins) MM_FIELD(skip_prologue) MM_FIELD(num_experts) MM_FIELD(topk)
     MM_FIELD(hidden) MM_FIELD(intermediate) MM_FIELD(max_tokens) MM_FIELD(workspace_bytes)
     MM_FIELD(x_sf) MM_FIELD(w1_sf) MM_FIELD(w2_sf) MM_FIELD(ffn_ue8m0) MM_FIELD(y_bf16)
+    MM_FIELD(fuse_l1l2)
 #undef MM_FIELD
     return -1;
 }

@@ -130,6 +130,7 @@ __device__ __forceinline__ v4i load16_stream(const uint8_t* p) {
 
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer resource word 3: 32-bit data format
 constexpr int kBufferNT = 2;               // buffer load cache policy bit: nt (non-temporal)
+constexpr int kBufferSc1 = 16;             // buffer load cache policy bit: sc1 (device scope)
 
 // The same non-temporal 16-byte weight load through a buffer resource over one
 // tile row: base and length in scalar registers, the lane's byte offset `off`
@@ -153,10 +154,13 @@ __device__ __forceinline__ v4i load16_row_stream(const uint8_t* row, int row_byt
 // whole 32-bit range from `base` (wave-uniform): the per-lane row offset in a
 // vector register, the k-step in a scalar one.  The callers' offsets stay
 // below 2^32 by the capacity limit the host enforces.
+// kAux: the load's cache-policy bits (0: cached; kBufferSc1: device-coherent,
+// for data another XCD wrote during the same launch).
+template <int kAux = 0>
 __device__ __forceinline__ v4i load16_rows(const uint8_t* base, uint32_t off, int soff) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(base), (short)0, -1, kBufferWord3);
-    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, kAux);
 }
 
 __device__ __forceinline__ v4i load16(const uint8_t* p) {

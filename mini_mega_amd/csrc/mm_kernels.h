@@ -30,6 +30,8 @@ constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 wor
 constexpr int kL2BlockN = 256;      // output channels per L2 workgroup
 constexpr int kStatusInts = 64;     // workspace status words
 constexpr int kStatusItemOverflow = fp8mega::kStatusItemOverflow;
+constexpr int kStatusWaitTimeout = fp8mega::kStatusWaitTimeout;
+constexpr int kReadySpinLimit = 1 << 20;   // default polls (~1 s with the sleep between)
 constexpr int kCutsL1 = 16;         // status[16..24]: XCD unit ranges of the L1 big GEMM
 constexpr int kCutsL2 = 32;         // status[32..40]: the same for L2
 // Tail queues of the big GEMMs: per XCD a ticket counter over the last
@@ -63,12 +65,18 @@ struct GemmParams {
     uint16_t* out16;          // L2: bf16 [P][H]
     int H, I, G, topk;
     int ffn_ue8m0;
+    // fused L1 -> L2 launch only (gemm_fused_kernel)
+    int* ready;               // [max_items]: L1 blocks done per work item
+    int ready_target;         // L1 blocks per item (L2 waits for this count)
+    int spin_limit;           // L2: polls of a ready counter before giving up
+    int* err;                 // status word [0]: kStatusWaitTimeout on give-up
 };
 
 template <int MT> __global__ void l1_kernel(GemmParams p);
 template <int MT> __global__ void l2_kernel(GemmParams p);
 __global__ void l1_big_kernel(GemmParams p);
 __global__ void l2_big_kernel(GemmParams p);
+__global__ void gemm_fused_kernel(GemmParams p1, GemmParams p2, int g1);
 
 __global__ void route_hist_kernel(const int64_t*, int, int, int, int*);
 __global__ void route_scan_kernel(const int64_t*, int, int, int*, int, int, int, int, int, int, int,

@@ -148,6 +148,8 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
         }
     }
     if (threadIdx.x < 2 * kQueueInts) status[kQueueL1 + threadIdx.x] = 0;   // tail queues
+    // per-item L1 ready counters of the fused L1 -> L2 launch (after the table)
+    for (int i = threadIdx.x; i < max_items; i += kScanThreads) items[4 * max_items + i] = 0;
     if (threadIdx.x == 0) {
         status[1] = min(nitems, max_items);
         status[2] = slots;

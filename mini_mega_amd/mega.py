@@ -129,6 +129,9 @@ class SymmBuffer:
         self._y_fp32 = torch.empty((cap, self.hidden), dtype=torch.float32, device="cuda")
         # also write the fp32 y next to a bf16 output (staged checks read it)
         self.write_fp32_y = False
+        # L1 and L2 in one launch, L2 units starting on an item once its L1
+        # units are done (MegaLaunchArgs::fuse_l1l2)
+        self.fuse_l1l2 = False
         self.launch_count = 0
 
     # -- workspace views (staged parity checks read these, as check.cu dumps
@@ -195,6 +198,7 @@ class SymmBuffer:
             a.y = None
         a.y_bf16 = y_bf16.data_ptr() if y_bf16 is not None else None
         a.skip_prologue = int(skip_prologue)
+        a.fuse_l1l2 = int(bool(self.fuse_l1l2))
         a.num_experts, a.topk = self.num_experts, self.num_topk
         a.hidden, a.intermediate = self.hidden, self.intermediate_hidden
         a.max_tokens = self.num_max_tokens_per_rank

@@ -216,3 +216,108 @@ def test_device_status_words():
     assert st["invalid_ids"] == 3
     assert st["dropped_by_capacity"] == valid - int(offsets[-1]) > 0
     assert st["items"] == int(r.status[1])
+
+
+def _outputs(buf, c, y):
+    slots = int(buf.offsets()[-1])
+    return (y.view(torch.int16).cpu().numpy(), buf.ffn(max(slots, 1)).cpu().numpy()[:slots],
+            buf.l2_out(max(slots, 1)).cpu().numpy()[:slots])
+
+
+@pytest.mark.parametrize("E,K,H,I,T,zipf,win,scaled", [
+    (32, 8, 1024, 512, 300, None, 0, True),
+    (64, 4, 2048, 768, 200, 1.1, 64, True),
+    (32, 8, 1024, 512, 300, None, 128, False),
+    (256, 8, 6144, 2048, 512, None, 0, True),
+    (256, 8, 6144, 2048, 2048, 1.1, 0, True),
+    (256, 8, 6144, 2048, 8192, None, 0, True),
+])
+def test_fused_l1l2_matches_two_launches(E, K, H, I, T, zipf, win, scaled):
+    """fuse_l1l2 (L1 and L2 in one launch, per-item ready counters): y, the
+    ffn bytes and the L2 rows are bit-identical to the two stream-ordered
+    launches, on small and full-size layers, skewed routing, fixed windows and
+    the raw (unscaled) path; no wait times out.  Then a launch reusing the
+    routing (skip_prologue, ready counters zeroed by the host path) and a
+    graph of two fused launches replayed twice give the same outputs."""
+    _say(f"fused L1->L2 E={E} T={T} zipf={zipf} win={win} scaled={scaled}")
+    c = mc.normal_case(E, K, H, I, T, seed=T + 7, scaled=scaled, zipf=zipf, win=win)
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I, expert_window=win)
+    _load(buf, c)
+    l1 = (c.w1, c.s1) if scaled else c.w1
+    l2 = (c.w2, c.s2) if scaled else c.w2
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    mm.fp8_mega_moe(y, l1, l2, buf)
+    torch.cuda.synchronize()
+    want = _outputs(buf, c, y)
+    buf.fuse_l1l2 = True
+    for rep in range(2):
+        y.zero_()
+        buf.workspace[int(buf.layout.ffn):].zero_()
+        mm.fp8_mega_moe(y, l1, l2, buf)
+        torch.cuda.synchronize()
+        got = _outputs(buf, c, y)
+        for g, w, name in zip(got, want, ("y", "ffn", "l2")):
+            assert np.array_equal(g, w), f"fused launch {rep}: {name} differs"
+        assert buf.device_status()["error"] == 0
+    # routing reused: the host zeroes the ready counters itself
+    y.zero_()
+    a = buf.make_args(T, l1, l2, y_bf16=y, skip_prologue=1)
+    assert mm.lib().mm_launch_full(ctypes.byref(a), _stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(_outputs(buf, c, y)[0], want[0]), "fused skip_prologue differs"
+    assert buf.device_status()["error"] == 0
+    # two fused launches as one graph, replayed twice
+    ys = [torch.empty((T, H), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for yy in ys:
+                mm.fp8_mega_moe(yy, l1, l2, buf)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(2):
+        for yy in ys:
+            yy.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for yy in ys:
+            assert np.array_equal(yy.view(torch.int16).cpu().numpy(), want[0]), \
+                f"fused graph replay {rep} differs"
+    buf.destroy()
+
+
+def test_fused_l1l2_bounded_wait_reports_timeout():
+    """With max_spins = 1 an L2 unit polls its item's ready counter once: the
+    launch still ends (every wait is bounded), and a unit that gave up sets
+    kStatusWaitTimeout, which read_status reports as a device error.  The
+    next launch with the default bound is exact again."""
+    _say("fused L1->L2 with max_spins=1")
+    E, K, H, I, T = 256, 8, 6144, 2048, 2048
+    c = mc.normal_case(E, K, H, I, T, seed=99, scaled=True)
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I)
+    _load(buf, c)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    mm.fp8_mega_moe(y, (c.w1, c.s1), (c.w2, c.s2), buf)
+    torch.cuda.synchronize()
+    want = y.view(torch.int16).cpu().numpy()
+    buf.fuse_l1l2 = True
+    a = buf.make_args(T, (c.w1, c.s1), (c.w2, c.s2), y_bf16=y)
+    a.max_spins = 1
+    assert mm.lib().mm_launch_full(ctypes.byref(a), _stream()) == 0
+    torch.cuda.synchronize()
+    st = buf.device_status()
+    out = (ctypes.c_int * 5)()
+    rc = mm.lib().mm_read_status(ctypes.byref(a), out, 5, _stream())
+    timed_out = bool(st["error"] & 2)
+    _say(f"  timeout bit set: {timed_out}")
+    assert st["error"] & ~2 == 0
+    assert rc == (7 if timed_out else 0)
+    if not timed_out:
+        assert np.array_equal(y.view(torch.int16).cpu().numpy(), want)
+    mm.fp8_mega_moe(y, (c.w1, c.s1), (c.w2, c.s2), buf)
+    torch.cuda.synchronize()
+    assert buf.device_status()["error"] == 0
+    assert np.array_equal(y.view(torch.int16).cpu().numpy(), want)
+    buf.destroy()
