@@ -1,6 +1,6 @@
 """Benchmark of the fused FP8xFP8 MoE layer on one MI355X.
 
-Workloads (BASELINE configs 1-4): E=256 experts, top-8, H=6144, I=2048, with
+Workloads: E=256 experts, top-8, H=6144, I=2048, with
 T = 512 (the headline, config 1), 2048, 8192 balanced and 2048 with a
 Zipf(1.1) router bias.  x bf16 N(0,1) -> per-token per-128 UE8M0 fp8, W1/W2
 N(0,0.02) fp8 with 128x128 UE8M0 block scales, softmax top-8 router on

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the MoE layer (the BASELINE workloads).
+"""Seeded synthetic inputs for the MoE layer (the benchmark and test workloads).
 
 * x: bf16 ~ N(0, 1) [T, H] cast to fp8 e4m3 with per-token per-128-column
   UE8M0 scales by the HIP quant_act kernel (or a direct RNE cast, unscaled).

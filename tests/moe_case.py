@@ -18,7 +18,7 @@ from oracle import oracle as orc
 L1_REL, L1_ABS = 7e-2, 2e-3
 L2_REL, L2_ABS = 1e-2, 1e-3
 RED_REL, RED_ABS = 1e-5, 1e-6
-# BASELINE end-to-end gate
+# end-to-end gate of the layer
 E2E_ABS_FRAC, E2E_COS = 2e-2, 0.9995
 
 

@@ -1,4 +1,4 @@
-"""Full-output end-to-end parity at BASELINE's full sizes: every T x H output
+"""Full-output end-to-end parity at the benchmark's full sizes: every T x H output
 of the layer against the oracle's whole chain (route -> L1 -> UE8M0 requant ->
 L2 -> bf16 -> reduce over all 256 experts), plus the share of L1 output bytes
 and L2 bf16 outputs that differ from the oracle's over ALL routed slots.

@@ -217,7 +217,7 @@ def test_dispatch_pool_is_gathered_rows():
 # ------------------------------------------------------------- the layer --
 SMALL = [
     # E, K, H, I, T, scaled, win
-    (8, 2, 256, 128, 32, True, 0),      # BASELINE config 0 (smoke)
+    (8, 2, 256, 128, 32, True, 0),      # the smoke workload
     (8, 2, 256, 128, 32, False, 0),
     (32, 8, 1024, 512, 200, True, 0),
     (32, 8, 1024, 512, 200, False, 16),
@@ -400,7 +400,7 @@ def test_checkcu_tk_fixed_routes_full_layer(launch):
 def test_real_decode_routes_full_layer(launch):
     """Routes of the reference's real GLM-5.2 decode corpus (test/76.real_decode/
     dataset.tk_info: the most skewed launch, a median one and the smallest)
-    through the full-size layer with BASELINE's scaled inputs: routing exact,
+    through the full-size layer with the benchmark's scaled inputs: routing exact,
     staged L1/L2 on the busiest, a median and the lightest active expert,
     REDUCE bit-exact, and the whole chain on a token subset."""
     from test_oracle import _tk_launches
@@ -428,7 +428,7 @@ def test_real_decode_routes_full_layer(launch):
 # ------------------------------------------------------------ full sizes --
 @pytest.mark.parametrize("T,zipf", [(512, None), (2048, None), (2048, 1.1), (8192, None)])
 def test_full_size_layer(T, zipf):
-    """BASELINE configs 1, 2, 4 at full size: routing exact, staged L1/L2 on
+    """The benchmark workloads at full size: routing exact, staged L1/L2 on
     the busiest / a median / the lightest expert, REDUCE bit-exact, and the
     whole chain on a token subset."""
     _say(f"full size T={T} zipf={zipf}")
