@@ -360,15 +360,19 @@ def e2e_metrics(got: np.ndarray, want: np.ndarray):
     return err, rms, cos
 
 
-def check_e2e(c: Case, r: Run, nthreads: int = 16):
-    """Whole chain vs the oracle's own chain (no device intermediates)."""
+def check_e2e(c: Case, r: Run, nthreads: int = 16, fp32_output: bool = False):
+    """Whole chain vs the oracle's own chain (no device intermediates).
+    fp32_output compares the device's fp32 sum instead of its bf16 cast (the
+    cast itself is checked bit for bit by check_reduce): with heavy slot-cap
+    drops the outputs are heavy-tailed, and the bf16 half-ulp of one output
+    at ~10x rms(y) alone exceeds 2e-2 rms(y) whatever the GEMMs did."""
     w1 = np.stack([c.w1_logical(e) for e in range(c.E)])
     w2 = np.stack([c.w2_logical(e) for e in range(c.E)])
     s1 = None if c.s1 is None else np.ascontiguousarray(c.s1.cpu().numpy())
     s2 = None if c.s2 is None else np.ascontiguousarray(c.s2.cpu().numpy())
     ref = orc.layer(c.x, c.xsf, w1, s1, w2, s2, c.idx, c.wts, E=c.E, G=c.G, scaled=c.scaled,
                     nthreads=nthreads, cap=c.cap if c.cap else None)
-    err, rms, cos = e2e_metrics(r.y, ref["y"])
+    err, rms, cos = e2e_metrics(r.y32 if fp32_output else r.y, ref["y"])
     print(f"[e2e] max_abs/rms={err / rms:.4f} cos={cos:.7f}", flush=True)
     assert err <= E2E_ABS_FRAC * rms and cos >= E2E_COS, (
         f"end-to-end: max_abs {err:.3e} rms {rms:.3e} cos {cos:.6f}")
