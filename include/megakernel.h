@@ -250,7 +250,7 @@ int mm_launch_full(const fp8mega::MegaLaunchArgs* a, void* stream);
 // (mm_noalloc_scratch_bytes() bytes, 64 MiB, one per GPU, held until the
 // process ends) instead of a->rwk, which is ignored with workspace_bytes:
 // the layout of a->max_tokens must fit it (kErrScratch otherwise; e.g. up to
-// ~540 tokens at E=256, top-8, H=6144, I=2048).  The caller still passes the
+// ~550 tokens at E=256, top-8, H=6144, I=2048).  The caller still passes the
 // inputs and outputs.  The call allocates nothing.  Every call on one GPU
 // shares that array: calls that overlap on one GPU (other streams, other
 // threads) race; skip_prologue reuses the previous call's routing.
