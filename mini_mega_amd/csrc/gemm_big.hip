@@ -31,7 +31,10 @@
 // Work units are numbered so that each XCD runs a contiguous range of them:
 // the N-blocks of one item share that XCD's L2 for the item's activations;
 // in L1 the last units of each range go out through a per-XCD ticket queue
-// that a few extra workgroups of the other XCDs also drain.
+// that a few extra workgroups of the other XCDs also drain.  The two GEMMs
+// run as two stream-ordered launches, or (gemm_fused_kernel, opt-in) as one
+// launch whose L2 units wait on per-item ready counters (reference:
+// src/compute_big.cuh:1948-1997).
 #include "mm_kernels.h"
 
 namespace mm {
