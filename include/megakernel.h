@@ -139,7 +139,7 @@ struct MegaLayout {
     int64_t chunk_hist;    // int32[nchunks][E] per-chunk histograms -> prefixes
     int64_t counts;        // int32[E]   per-expert routed rows (after cap)
     int64_t offsets;       // int32[E+1] exclusive prefix of counts
-    int64_t items;         // int32[max_items][4] (expert, first row, end row, j | n << 16) work
+    int64_t items;         // int32[max_items][4] (expert, first slot, end slot, j | n << 16) work
                            // items, then int32[max_items] per-item L1 ready counters (fuse_l1l2)
     int64_t perm;          // uint32[P]  pair index per slot (canonical order)
     int64_t pair_pos;      // int32[P]   slot per pair or -1

@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
     if (item >= p.status[1]) return;
     const int4 it = reinterpret_cast<const int4*>(p.items)[item];
     const int e = it.x, m0 = it.y;
-    const int cnt = it.z, off = p.offsets[e];  // rows m0 .. cnt-1 of expert e
+    const int cnt = it.z;  // slots m0 .. cnt-1 (absolute) of expert e
     const int rows = cnt - m0;
     const int ntiles = (rows + 15) >> 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -149,13 +149,13 @@ __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
         wsf1 = se + (size_t)(ntu >> 3) * KT;
     }
 
-    // Token rows (B operand): row m0+16j+L%16 of expert e's slots.
+    // Token rows (B operand): slot m0+16j+L%16 (absolute) of expert e.
     const uint8_t* xr[MT];
     const uint8_t* xsf[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
         const int r = m0 + 16 * j + (lane & 15);
-        const int slot = off + (r < cnt ? r : 0);
+        const int slot = r < cnt ? r : 0;
         const size_t tok = p.perm[slot] / (uint32_t)p.topk;
         xr[j] = p.x + tok * H + 32 * (lane >> 4);
         xsf[j] = p.x_sf ? p.x_sf + tok * KT : nullptr;
@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
             const uint32_t sb = block_scale_byte(amax);
             const float inv = inv_scale(sb);
             if (j < ntiles && r < cnt) {
-                const size_t slot = (size_t)(off + r);
+                const size_t slot = (size_t)r;
 #pragma unroll
                 for (int pp = 0; pp < 2; ++pp) {
                     const uint32_t q = pack4_fp8(hv[j][pp][0] * inv, hv[j][pp][1] * inv,
@@ -222,7 +222,7 @@ __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
         for (int j = 0; j < MT; ++j) {
             const int r = m0 + 16 * j + (lane & 15);
             if (j < ntiles && r < cnt) {
-                const size_t slot = (size_t)(off + r);
+                const size_t slot = (size_t)r;
 #pragma unroll
                 for (int pp = 0; pp < 2; ++pp) {
                     const uint32_t q =
@@ -241,7 +241,7 @@ __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
     if (item >= p.status[1]) return;
     const int4 it = reinterpret_cast<const int4*>(p.items)[item];
     const int e = it.x, m0 = it.y;
-    const int cnt = it.z, off = p.offsets[e];  // rows m0 .. cnt-1 of expert e
+    const int cnt = it.z;  // slots m0 .. cnt-1 (absolute) of expert e
     const int rows = cnt - m0;
     const int ntiles = (rows + 15) >> 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
         const int r = m0 + 16 * j + (lane & 15);
-        const size_t slot = (size_t)(off + (r < cnt ? r : 0));
+        const size_t slot = (size_t)(r < cnt ? r : 0);
         xr[j] = p.x + slot * I + 32 * (lane >> 4);
         xsf[j] = p.x_sf ? p.x_sf + slot * KT : nullptr;
     }
@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
     for (int j = 0; j < MT; ++j) {
         const int r = m0 + 16 * j + (lane & 15);
         if (j < ntiles && r < cnt) {
-            const size_t slot = (size_t)(off + r);
+            const size_t slot = (size_t)r;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 uint2 v;

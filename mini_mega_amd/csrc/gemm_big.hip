@@ -322,7 +322,7 @@ __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSme
 
 // Per-unit context shared by the two kernels.
 struct BigItem {
-    int e, m0, rows, off, bx, item;
+    int e, m0, rows, bx, item;   // m0: first slot (absolute)
 };
 
 // Work units: an expert with n items has n * nb units, numbered from
@@ -396,18 +396,19 @@ __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& i
         u = *s_unit;
         if (u < 0) return false;
     }
+    // One dependent load for an expert of one item (every expert up to
+    // 256 rows), a second one otherwise; the items hold absolute slots.
     const int4* items = reinterpret_cast<const int4*>(p.items);
     const int im = u / nb;                 // item-major item: same expert
-    const int jn = items[im].w;
-    const int i0 = im - (jn & 0xffff), n = jn >> 16;
+    int4 v = items[im];
+    const int i0 = im - (v.w & 0xffff), n = v.w >> 16;
     const int local = u - nb * i0;
     it.bx = local / n;
     it.item = i0 + local % n;
-    const int4 v = items[it.item];
+    if (n != 1) v = items[it.item];
     it.e = v.x;
     it.m0 = v.y;
     it.rows = v.z - v.y;
-    it.off = p.offsets[it.e];
     return true;
 }
 
@@ -572,7 +573,7 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
             const uint32_t sb = block_scale_byte(amax);
             const float inv = inv_scale(sb);
             if (r < it.rows) {
-                const size_t slot = (size_t)(it.off + it.m0 + r);
+                const size_t slot = (size_t)(it.m0 + r);
 #pragma unroll
                 for (int c = 0; c < kH; ++c)
                     put4(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4),
@@ -592,7 +593,7 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
         for (int j = 0; j < NT; ++j) {
             const int r = 16 * j + (lane & 15);
             if (r < it.rows) {
-                const size_t slot = (size_t)(it.off + it.m0 + r);
+                const size_t slot = (size_t)(it.m0 + r);
 #pragma unroll
                 for (int c = 0; c < kH; ++c)
                     put4(p.out8 + slot * I + hw + 16 * c + 4 * (lane >> 4),
@@ -625,7 +626,7 @@ __device__ __forceinline__ void l1_big(const GemmParams& p, BigSmem& sm, int* s_
         big_load_scales<W>(
             sm, KT, min(tiles * 16, kBigRows), p.w_sf != nullptr,
             [&](int r) -> const uint8_t* {
-                const int slot = it.off + it.m0 + (r < it.rows ? r : 0);
+                const int slot = it.m0 + (r < it.rows ? r : 0);
                 const uint32_t tok = p.perm[slot] / (uint32_t)p.topk;
                 sm.tok[r] = tok;
                 return p.x_sf ? p.x_sf + (size_t)tok * KT : nullptr;
@@ -669,7 +670,7 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     XLoader<W, NT, kFused ? kBufferSc1 : 0> xl;
     xl.base = p.x;
     big_loader_init(xl, [&](int r) {
-        return (uint32_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
+        return (uint32_t)(it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
     });
     v4f acc[kWT][NT];
     big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
@@ -677,7 +678,7 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     for (int j = 0; j < NT; ++j) {
         const int r = 16 * j + (lane & 15);
         if (r < it.rows) {
-            uint16_t* dst = p.out16 + (size_t)(it.off + it.m0 + r) * H + n0 + 4 * (lane >> 4);
+            uint16_t* dst = p.out16 + (size_t)(it.m0 + r) * H + n0 + 4 * (lane >> 4);
 #pragma unroll
             for (int t = 0; t < kWT; ++t) {
                 uint2 v;
@@ -719,7 +720,7 @@ __device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_
         big_load_scales<W, kFused>(
             sm, KT, min(tiles * 16, kBigRows), p.w_sf != nullptr,
             [&](int r) -> const uint8_t* {
-                return p.x_sf ? p.x_sf + (size_t)(it.off + it.m0 + (r < it.rows ? r : 0)) * KT
+                return p.x_sf ? p.x_sf + (size_t)(it.m0 + (r < it.rows ? r : 0)) * KT
                               : nullptr;
             },
             [&](int t) {

@@ -54,7 +54,7 @@ struct GemmParams {
     const uint8_t* w_sf;      // UE8M0 block scales [E][N/128][K/128] or null
     const int* counts;        // [E]
     const int* offsets;       // [E+1]
-    const int* items;         // [max_items][4]: expert, first row, end row, j | n << 16
+    const int* items;         // [max_items][4]: expert, first slot, end slot (absolute), j | n << 16
                               // (item j of the expert's n)
     const int* status;        // [1] = number of items
     const int* xcd_cuts;      // [9]: XCD x runs big-GEMM units [cuts[x], cuts[x+1])

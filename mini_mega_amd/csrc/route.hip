@@ -134,8 +134,10 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     // and all but the first take it from L2.  (Measured on MI355X at T =
     // 8192: splitting at 16-row multiples instead ran 2% less MFMA work but
     // its unequal items drifted apart; L1 fetched 9.30 vs 7.33 GB and the
-    // layer took 4908-4943 vs 4841-4854 us.)  Record: (expert, first row,
-    // end row, index within the expert | item count of the expert << 16).
+    // layer took 4908-4943 vs 4841-4854 us.)  Record: (expert, first slot,
+    // end slot, index within the expert | item count of the expert << 16),
+    // the slots absolute (the expert's offset included), so that a GEMM unit
+    // needs no offsets[] load after its item.
     const int nm = (cnt + m_tile - 1) / m_tile;
     const int sz = nm > 0 ? (cnt + nm - 1) / nm : 0;
     int nitems = 0;
@@ -144,7 +146,8 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
         const int it = ioff + j;
         if (it < max_items) {
             const int m0 = j * sz;
-            reinterpret_cast<int4*>(items)[it] = make_int4(e, m0, min(cnt, m0 + sz), j | (nm << 16));
+            reinterpret_cast<int4*>(items)[it] =
+                make_int4(e, off + m0, off + min(cnt, m0 + sz), j | (nm << 16));
         }
     }
     if (threadIdx.x < 2 * kQueueInts) status[kQueueL1 + threadIdx.x] = 0;   // tail queues

@@ -165,7 +165,7 @@ class SymmBuffer:
         return self._ws(self.layout.status, torch.int32, (64,))
 
     def items(self, n: int):
-        """Work items: (expert, first row, end row, j | n << 16 for item j of
+        """Work items: (expert, first slot, end slot, j | n << 16 for item j of
         the expert's n)."""
         return self._ws(self.layout.items, torch.int32, (n, 4))
 

@@ -145,14 +145,16 @@ def check_routing(c: Case, r: Run):
     assert np.array_equal(r.perm, perm), "canonical permutation differs"
     assert np.array_equal(r.pair_pos, pair_pos), "pair slots differ"
     assert r.status[0] == 0, f"device status word {r.status[0]}"
-    # work items: each expert's rows split evenly into ceil(count / m_tile) items
+    # work items: each expert's rows split evenly into ceil(count / m_tile)
+    # items, recorded as absolute slot ranges
     m_tile = int(r.buf.layout.m_tile)
     want = []
     for e, cnt in enumerate(counts.tolist()):
         if cnt == 0:
             continue
         nm, sz = item_split(cnt, m_tile)
-        want += [(e, j * sz, min(cnt, (j + 1) * sz), j | (nm << 16)) for j in range(nm)]
+        o = int(offsets[e])
+        want += [(e, o + j * sz, o + min(cnt, (j + 1) * sz), j | (nm << 16)) for j in range(nm)]
     assert int(r.status[1]) == len(want), "work item count differs"
     got = r.buf.items(len(want)).cpu().numpy() if want else np.zeros((0, 4), np.int32)
     assert np.array_equal(got, np.array(want, dtype=np.int32).reshape(-1, 4)), "work items differ"
