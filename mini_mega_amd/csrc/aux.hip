@@ -200,7 +200,7 @@ convert_selftest_kernel(const float* __restrict__ in, int n, uint8_t* __restrict
     if (i >= n) return;
     const float v = in[i];
     if (out8) out8[i] = (uint8_t)(pack4_fp8(v, 0.f, 0.f, 0.f) & 0xFFu);
-    if (out16) out16[i] = (uint16_t)bf16_rne(v);
+    if (out16) out16[i] = (uint16_t)(pack2_bf16(v, 0.0f) & 0xFFFFu);   // the GEMM epilogue's conversion
 }
 
 __global__ void empty_kernel() {}

@@ -178,7 +178,7 @@ __global__ void __launch_bounds__(kGemmThreads) l1_kernel(GemmParams p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float g = acc[pp][j][i], u = acc[2 + pp][j][i];
-                hv[j][pp][i] = (g / (1.0f + __expf(-g))) * u;
+                hv[j][pp][i] = silu_mul(g, u);
             }
 
     const int I128 = I >> 7;
@@ -282,8 +282,8 @@ __global__ void __launch_bounds__(kGemmThreads) l2_kernel(GemmParams p) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 uint2 v;
-                v.x = bf16_rne(acc[t][j][0]) | (bf16_rne(acc[t][j][1]) << 16);
-                v.y = bf16_rne(acc[t][j][2]) | (bf16_rne(acc[t][j][3]) << 16);
+                v.x = pack2_bf16(acc[t][j][0], acc[t][j][1]);
+                v.y = pack2_bf16(acc[t][j][2], acc[t][j][3]);
                 *reinterpret_cast<uint2*>(p.out16 + slot * H + n0 + 16 * t + 4 * (lane >> 4)) = v;
             }
         }

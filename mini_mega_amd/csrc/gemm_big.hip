@@ -545,7 +545,7 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float g = acc[c][j][i], u = acc[c + kH][j][i];
-                hv[c][j][i] = (g / (1.0f + __expf(-g))) * u;
+                hv[c][j][i] = silu_mul(g, u);
             }
     const int I128 = I >> 7;
     if (p.ffn_ue8m0) {
@@ -682,8 +682,8 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
 #pragma unroll
             for (int t = 0; t < kWT; ++t) {
                 uint2 v;
-                v.x = bf16_rne(acc[t][j][0]) | (bf16_rne(acc[t][j][1]) << 16);
-                v.y = bf16_rne(acc[t][j][2]) | (bf16_rne(acc[t][j][3]) << 16);
+                v.x = pack2_bf16(acc[t][j][0], acc[t][j][1]);
+                v.y = pack2_bf16(acc[t][j][2], acc[t][j][3]);
                 *reinterpret_cast<uint2*>(dst + 16 * t) = v;
             }
         }

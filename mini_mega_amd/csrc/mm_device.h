@@ -103,6 +103,22 @@ __device__ __forceinline__ uint32_t bf16_rne(float v) {
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Two fp32 -> packed bf16 (a low, b high) with gfx950's v_cvt_pk_bf16_f32, which
+// rounds to nearest even: equal to bf16_rne for every non-NaN input (checked on
+// MI355X over all 2^32 bit patterns; a NaN becomes a quiet NaN).  One VALU
+// instruction per pair instead of ~5 per value.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+    typedef float v2f_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f_t){a, b}, v2bf_t));
+}
+
+// SwiGLU's silu(g) * u, with the sigmoid's reciprocal from v_rcp_f32 (1 ulp)
+// instead of an IEEE division (a dozen instructions per value).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 // UE8M0 exponent byte of the power of two >= |x| (ceil), clamped to [1, 254].

@@ -57,6 +57,25 @@ def test_device_fp8_and_bf16_conversion_bit_exact():
     torch.cuda.synchronize()
     assert np.array_equal(o8.cpu().numpy(), orc.e4m3_quantize(v))
     assert np.array_equal(o16.cpu().numpy().view(np.uint16), orc.f32_to_bf16(v))
+    # bf16 rounding (the GEMM epilogue's v_cvt_pk_bf16_f32) on random fp32 bit
+    # patterns, exact bf16 ties and their neighbours, denormals and the overflow
+    # edge; NaN is excluded (the hardware quiets it, the reference keeps its bits)
+    bits = rng.integers(0, 2**32, size=200000, dtype=np.uint64).astype(np.uint32)
+    hb = rng.integers(0, 2**16, size=50000, dtype=np.uint64).astype(np.uint32) << 16
+    ties = np.concatenate([hb | 0x8000, (hb | 0x8000) + 1, (hb | 0x8000) - 1, hb | 0x7FFF])
+    edge = np.array([0x00000001, 0x00008000, 0x007FFFFF, 0x00800000, 0x7F7F7FFF, 0x7F7F8000,
+                     0x7F7FFFFF, 0x7F800000, 0xFF800000, 0x80000001, 0xFF7FFFFF],
+                    dtype=np.uint32)
+    u = np.concatenate([bits, ties, edge])
+    u = u[(u & 0x7FFFFFFF) <= 0x7F800000]
+    vb = u.view(np.float32)
+    srcb = torch.from_numpy(vb.copy()).cuda()
+    o8b = torch.empty(vb.size, dtype=torch.uint8, device="cuda")
+    o16b = torch.empty(vb.size, dtype=torch.int16, device="cuda")
+    assert mm.lib().mm_selftest_convert(srcb.data_ptr(), vb.size, o8b.data_ptr(), o16b.data_ptr(),
+                                        _stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(o16b.cpu().numpy().view(np.uint16), orc.f32_to_bf16(vb))
 
 
 def test_pack_weights_roundtrip():
