@@ -64,6 +64,7 @@ enum MegaStatus : int {
 //   [1]  work items, [2] routed slots,
 //   [3]  pairs dropped by slot_capacity,
 //   [4]  pairs whose expert id is outside [0, num_experts) (dropped)
+//   [5]  rows of the largest work item (the L2 walk runs when 33..128)
 //   [16..24], [32..40] the big GEMMs' XCD unit ranges (L1, L2)
 // The reference returns no status (src/megakernel.h:117-130): its launches
 // are void and its host CHECKs exit (src/host_layout.cuh:18-26).
@@ -128,6 +129,10 @@ struct MegaLaunchArgs {
                                            // ready counters; reference src/compute_big.cuh:
                                            // 1948-1997).  Windows > 32 rows; max_spins > 0
                                            // bounds each wait (else ~1 s).
+    int l2_no_walk = 0;                    // 1: L2 always one unit per workgroup; 0: when the
+                                           // largest work item has 3-8 token tiles, one
+                                           // workgroup per CU walks the units, streaming
+                                           // the next unit's weights during the current one
 };
 
 // Byte offsets of every region inside the workspace (the single-GPU

@@ -75,18 +75,29 @@ struct alignas(16) BigSmem {
 // flight while kt+1 is written to LDS; with one (above 12 token tiles, where
 // registers go to accumulators, and a k-step's 4*NT MFMA groups alone cover
 // an L2 hit; measured even with two at T = 8192), kt+1 is loaded during kt.
-template <int W, int NT, int kAux = 0>
+template <int W, int NT, int kAux = 0, bool kOpaqueTid = false>
 struct XLoader {
     static constexpr int kThreads = Geo<W>::kThreads;
     static constexpr int U = (NT * 128 + kThreads - 1) / kThreads;
     static constexpr int XS = NT <= 12 ? 2 : 1;
     const uint8_t* base;
+    int tid_;   // kOpaqueTid: the thread index, read once per unit through an empty asm
     uint32_t off[U];
     v4i reg[XS][U];
 
-    __device__ __forceinline__ static int chunk(int u) {
-        return (threadIdx.x + kThreads * u) % (NT * 128);
+    __device__ __forceinline__ int tid() const {
+        if constexpr (kOpaqueTid) {
+            __builtin_assume(tid_ >= 0 && tid_ < kThreads);
+            return tid_;
+        } else {
+            return threadIdx.x;
+        }
     }
+    // the wave index, wave-uniform (in a scalar register)
+    __device__ __forceinline__ int wave() const {
+        return __builtin_amdgcn_readfirstlane(tid() >> 6);
+    }
+    __device__ __forceinline__ int chunk(int u) const { return (tid() + kThreads * u) % (NT * 128); }
     __device__ __forceinline__ static int row_of(int i) { return ((i >> 7) << 4) | (i & 15); }
     __device__ __forceinline__ static int cc_of(int i) { return (i >> 4) & 7; }
     __device__ __forceinline__ static int slot_of(int i) {
@@ -135,8 +146,7 @@ __device__ __forceinline__ v8bf w_group(const WStage<WT>& w, int t, int q, float
 
 // The wave's weight-tile scale bytes of k-step kt (byte t = tile t).
 template <int WT>
-__device__ __forceinline__ uint32_t w_scales(const BigSmem& sm, int kt) {
-    const int wave = threadIdx.x >> 6;
+__device__ __forceinline__ uint32_t w_scales(const BigSmem& sm, int kt, int wave) {
     if constexpr (WT == 2)
         return *reinterpret_cast<const uint16_t*>(&sm.sfw[kt][WT * wave]);
     else
@@ -172,6 +182,20 @@ constexpr int big_read_ahead() { return (W == 8 && NT > 12) ? 2 : 3; }
 // keep the later issue (at NT = 16 the early stages also made the body spill).
 constexpr int kEarlyMaxTiles = 2;
 
+// The next unit's weight tiles, for a workgroup that runs several units in a
+// row (l2_walk): the last S - 1 k-steps of a unit issue the next unit's first
+// weight stages where they would otherwise reload the unit's last k-step, so
+// the weight stream runs on across the unit boundary.  NoNext: one unit.
+struct NoNext {
+    static constexpr bool kOn = false;
+};
+template <int WT>
+struct NextW {
+    static constexpr bool kOn = true;
+    WTiles<WT> wt;
+    bool has;
+};
+
 // One k-step, software-pipelined by hand.  The step's 4*NT chunks (k-group
 // q, token tile j) each hold: the LDS read of the activation operand D
 // chunks ahead, a share of the conversions of the next k-group's weight
@@ -185,25 +209,38 @@ constexpr int kEarlyMaxTiles = 2;
 // compiler's wait counts stay partial).  After: the barrier that publishes
 // the committed activations.  a0 carries the converted k-group-0 operand from
 // one step to the next.
-template <int W, int NT, int S, int s, class XL>
+template <int W, int NT, int S, int s, class XL, class NX = NoNext>
 __device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                          XL& xl, WStage<Geo<W>::kWT> (&w)[S],
                                          const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
-                                         int kt, int KT) {
+                                         int kt, int KT, const NX& nx = NX{}) {
     constexpr int kWT = Geo<W>::kWT;
     constexpr int XS = XL::XS, U = XL::U;
     constexpr int G = 4 * NT, D = big_read_ahead<W, NT>() < G ? big_read_ahead<W, NT>() : G;
     constexpr int rs = XS == 2 ? ((s + 1) & 1) : 0;   // register stage holding k-step kt+1
-    const int lane = threadIdx.x & 63;
+    const int lane = xl.tid() & 63, wave = xl.wave();
     // weights first: vector loads complete in issue order, so the wait for
     // the next step's weights (end of this step) must not also wait for this
     // step's gathered activation rows, which can miss to HBM (measured:
     // T = 8192 L1 3136 vs 3252 us)
-    w_load<kWT>(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));
-    xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
+    // when walking (L2 units only): the activation rows first, so that the
+    // commit's wait does not also wait for the weights issued ahead of them
+    // (measured on MI355X with the walk at T = 2048: L2 610-611 vs 615-618 us)
+    if constexpr (NX::kOn) xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
+    if constexpr (NX::kOn) {
+        const int kw = kt + S - 1;
+        const bool cur = kw < KT, nxt = !cur && nx.has;
+        WTiles<kWT> ws = wt;
+#pragma unroll
+        for (int t = 0; t < kWT; ++t) ws.row[t] = nxt ? nx.wt.row[t] : wt.row[t];
+        w_load<kWT>(w[(s + S - 1) % S], ws, cur ? kw : nxt ? kw - KT : KT - 1);
+    } else {
+        w_load<kWT>(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));
+    }
+    if constexpr (!NX::kOn) xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
     // scale bytes, read here and decoded where used (no wait before the MFMAs)
     const int kn = min(kt + 1, KT - 1);
-    const uint32_t sc = w_scales<kWT>(sm, kt), sn = w_scales<kWT>(sm, kn);
+    const uint32_t sc = w_scales<kWT>(sm, kt, wave), sn = w_scales<kWT>(sm, kn, wave);
     uint32_t xs[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -257,24 +294,24 @@ __device__ __forceinline__ void big_step(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& s
     __syncthreads();
 }
 
-template <int W, int NT, int S, int s, class XL>
+template <int W, int NT, int S, int s, class XL, class NX>
 __device__ __forceinline__ void big_group(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                           XL& xl, WStage<Geo<W>::kWT> (&w)[S],
                                           const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
-                                          int kb, int KT) {
-    big_step<W, NT, S, s>(acc, sm, xl, w, wt, a0, kb + s, KT);
-    if constexpr (s + 1 < S) big_group<W, NT, S, s + 1>(acc, sm, xl, w, wt, a0, kb, KT);
+                                          int kb, int KT, const NX& nx) {
+    big_step<W, NT, S, s>(acc, sm, xl, w, wt, a0, kb + s, KT, nx);
+    if constexpr (s + 1 < S) big_group<W, NT, S, s + 1>(acc, sm, xl, w, wt, a0, kb, KT, nx);
 }
 
 // The KT % S remaining k-steps, one guarded step each.
-template <int W, int NT, int S, int r, class XL>
+template <int W, int NT, int S, int r, class XL, class NX>
 __device__ __forceinline__ void big_tail(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                          XL& xl, WStage<Geo<W>::kWT> (&w)[S],
                                          const WTiles<Geo<W>::kWT>& wt, v8bf (&a0)[Geo<W>::kWT],
-                                         int KF, int KT) {
+                                         int KF, int KT, const NX& nx) {
     if (KF + r < KT) {
-        big_step<W, NT, S, r>(acc, sm, xl, w, wt, a0, KF + r, KT);
-        if constexpr (r + 2 < S) big_tail<W, NT, S, r + 1>(acc, sm, xl, w, wt, a0, KF, KT);
+        big_step<W, NT, S, r>(acc, sm, xl, w, wt, a0, KF + r, KT, nx);
+        if constexpr (r + 2 < S) big_tail<W, NT, S, r + 1>(acc, sm, xl, w, wt, a0, KF, KT, nx);
     }
 }
 
@@ -291,10 +328,13 @@ __device__ __forceinline__ void w_prologue(WStage<WT> (&w)[S], const WTiles<WT>&
 
 // kEarly: the caller issued the first weight stages (w_prologue) before the
 // unit's scale staging, so that their HBM latency overlaps it.
-template <int W, int NT, int S, bool kEarly, class XL>
+// NX::kOn (several units per workgroup): the previous unit issued the first
+// `pref` weight stages already; the prologue issues the rest.
+template <int W, int NT, int S, bool kEarly, class XL, class NX = NoNext>
 __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
                                              XL& xl, const WTiles<Geo<W>::kWT>& wt,
-                                             int KT, WStage<Geo<W>::kWT> (&w)[S]) {
+                                             int KT, WStage<Geo<W>::kWT> (&w)[S],
+                                             const NX& nx = NX{}, int pref = 0) {
     constexpr int kWT = Geo<W>::kWT;
     constexpr int XS = XL::XS;
     static_assert(XS == 1 || S % 2 == 0, "two activation stages alternate within a group");
@@ -305,19 +345,25 @@ __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSme
         for (int j = 0; j < NT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
     xl.issue(0, 0);
     if constexpr (XS == 2) xl.issue(min(1, KT - 1), 1);
-    if constexpr (!kEarly) w_prologue<kWT, S>(w, wt, KT);
+    if constexpr (NX::kOn) {
+#pragma unroll
+        for (int j = 0; j < S - 1; ++j)
+            if (j >= pref) w_load<kWT>(w[j], wt, min(j, KT - 1));
+    } else if constexpr (!kEarly) {
+        w_prologue<kWT, S>(w, wt, KT);
+    }
     xl.commit(sm, 0, 0, 0);
     __syncthreads();
     v8bf a0[kWT];
     {
-        const uint32_t sc = w_scales<kWT>(sm, 0);
+        const uint32_t sc = w_scales<kWT>(sm, 0, xl.wave());
 #pragma unroll
         for (int t = 0; t < kWT; ++t) a0[t] = w_group<kWT>(w[0], t, 0, scale_of(sc, t));
     }
     const int KF = KT - KT % S;
 #pragma unroll 1
-    for (int kb = 0; kb < KF; kb += S) big_group<W, NT, S, 0>(acc, sm, xl, w, wt, a0, kb, KT);
-    big_tail<W, NT, S, 0>(acc, sm, xl, w, wt, a0, KF, KT);
+    for (int kb = 0; kb < KF; kb += S) big_group<W, NT, S, 0>(acc, sm, xl, w, wt, a0, kb, KT, nx);
+    big_tail<W, NT, S, 0>(acc, sm, xl, w, wt, a0, KF, KT, nx);
 }
 
 // Per-unit context shared by the two kernels.
@@ -426,9 +472,10 @@ __device__ __forceinline__ bool big_unit(const GemmParams& p, int nb, BigItem& i
 // (the fused L1 -> L2 handoff) and are read at device scope.
 template <int W, bool kCoherent = false, class RowF, class TileF>
 __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, bool has_w,
-                                                RowF row_scale, TileF tile_scale) {
+                                                RowF row_scale, TileF tile_scale,
+                                                int tid = threadIdx.x) {
     constexpr int T = Geo<W>::kThreads;
-    for (int r = threadIdx.x; r < nrows; r += T) {
+    for (int r = tid; r < nrows; r += T) {
         const uint8_t* src = row_scale(r);
         uint8_t* dst = &sm.sfx[r][0];
         if (src && (KT & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
@@ -444,7 +491,7 @@ __device__ __forceinline__ void big_load_scales(BigSmem& sm, int KT, int nrows, 
             for (int k = 0; k < KT; k += 4) *reinterpret_cast<uint32_t*>(dst + k) = 0x7f7f7f7fu;
         }
     }
-    for (int i = threadIdx.x; i < kBlockTiles * KT; i += T) {
+    for (int i = tid; i < kBlockTiles * KT; i += T) {
         const int t = i % kBlockTiles, k = i / kBlockTiles;
         sm.sfw[k][t] = has_w ? tile_scale(t)[k] : (uint8_t)127;
     }
@@ -481,7 +528,7 @@ template <class XL, class RowOff>
 __device__ __forceinline__ void big_loader_init(XL& xl, RowOff row_off) {
 #pragma unroll
     for (int u = 0; u < XL::U; ++u) {
-        const int i = XL::chunk(u);
+        const int i = xl.chunk(u);
         xl.off[u] = row_off(XL::row_of(i)) + XL::cc_of(i) * 16;
     }
 }
@@ -736,7 +783,147 @@ __device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_
 __global__ void __launch_bounds__(512) l2_big_kernel(GemmParams p) {
     __shared__ BigSmem sm;
     __shared__ int s_unit;
+    if (walk_taken(p)) return;   // the walk (launched just before) ran the units
     l2_big<8, false>(p, sm, &s_unit, blockIdx.x, gridDim.x);
+}
+
+// ------------------------------------------------------------- L2 walker --
+// One workgroup per CU walks its XCD's unit range at a stride of the XCD's
+// workgroup count.  A unit's last k-steps issue the next unit's first weight
+// stages (NextW), so the CU's weight stream does not drain at the unit
+// boundary: the next unit's scale staging and first activation commit wait for
+// loads that were issued during the previous unit, and no workgroup is
+// dispatched in between.  Weight stages: 4 up to 12 token tiles, 2 above (both
+// divide K / 128 = 16 k-steps, so the ring's slots line up across units).
+
+// (item, block) of unit u, as big_unit decodes it.
+__device__ __forceinline__ BigItem walk_unit(const GemmParams& p, int nb, int u) {
+    BigItem it;
+    const int4* items = reinterpret_cast<const int4*>(p.items);
+    const int im = u / nb;
+    int4 v = items[im];
+    const int i0 = im - (v.w & 0xffff), n = v.w >> 16;
+    const int local = u - nb * i0;
+    it.bx = local / n;
+    it.item = i0 + local % n;
+    if (n != 1) v = items[it.item];
+    it.e = v.x;
+    it.m0 = v.y;
+    it.rows = v.z - v.y;
+    return it;
+}
+
+template <int W>
+__device__ __forceinline__ WTiles<Geo<W>::kWT> l2_tiles(const GemmParams& p, const BigItem& it,
+                                                          int wave, int lane) {
+    constexpr int kWT = Geo<W>::kWT;
+    const int n0 = it.bx * kL2BlockN + wave * (kL2BlockN / W);
+    const uint8_t* we = p.w + (size_t)it.e * (size_t)p.H * p.I;
+    WTiles<kWT> wt;
+    wt.KT = p.I >> 7;
+#pragma unroll
+    for (int t = 0; t < kWT; ++t) wt.set(t, we, (n0 >> 4) + t, lane);
+    return wt;
+}
+
+
+// One unit of the walk.  w: the weight ring (4 stages; bodies of 2 stages use
+// its first two); pref: stages of this unit the previous one issued; nx: the
+// next unit.  The thread index goes through an empty asm once per unit, so that
+// the optimiser does not hoist every body's thread-index arithmetic out of the
+// walk (where it stays live across all sixteen bodies and spills).
+template <int W, int NT>
+__device__ __forceinline__ void l2_walk_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
+                                             WStage<Geo<W>::kWT> (&ring)[4],
+                                             const NextW<Geo<W>::kWT>& nx, int pref) {
+    constexpr int kWT = Geo<W>::kWT;
+    constexpr int S = kWalkStages;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    __builtin_assume(tid >= 0 && tid < Geo<W>::kThreads);
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int H = p.H, I = p.I, KT = I >> 7;
+    const WTiles<kWT> wt = l2_tiles<W>(p, it, wave, lane);
+    const int tiles = (it.rows + 15) >> 4;
+    big_load_scales<W>(
+        sm, KT, min(tiles * 16, kBigRows), p.w_sf != nullptr,
+        [&](int r) -> const uint8_t* {
+            return p.x_sf ? p.x_sf + (size_t)(it.m0 + (r < it.rows ? r : 0)) * KT : nullptr;
+        },
+        [&](int t) {
+            const int n = it.bx * kL2BlockN + t * 16;
+            return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
+        },
+        tid);
+    XLoader<W, NT, 0, true> xl;
+    xl.base = p.x;
+    xl.tid_ = tid;
+    big_loader_init(xl, [&](int r) {
+        return (uint32_t)(it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
+    });
+    v4f acc[kWT][NT];
+    big_mainloop<W, NT, S, false>(acc, sm, xl, wt, KT, ring, nx, pref);
+    const int n0 = it.bx * kL2BlockN + wave * (kL2BlockN / W);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int r = 16 * j + (lane & 15);
+        if (r < it.rows) {
+            uint16_t* dst = p.out16 + (size_t)(it.m0 + r) * H + n0 + 4 * (lane >> 4);
+#pragma unroll
+            for (int t = 0; t < kWT; ++t) {
+                uint2 v;
+                v.x = pack2_bf16(acc[t][j][0], acc[t][j][1]);
+                v.y = pack2_bf16(acc[t][j][2], acc[t][j][3]);
+                *reinterpret_cast<uint2*>(dst + 16 * t) = v;
+            }
+        }
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void l2_walk(const GemmParams& p, BigSmem& sm, int L, int grid) {
+    constexpr int kWT = Geo<W>::kWT;
+    const int x = L & 7, k = L >> 3, stride = (grid - x + 7) >> 3;
+    const int lo = p.xcd_cuts[x], hi = p.xcd_cuts[x + 1];
+    int u = lo + k;
+    if (u >= hi) return;
+    const int nb = p.H / kL2BlockN;
+    BigItem it = walk_unit(p, nb, u);
+    WStage<kWT> ring[4];
+    int pref = 0;
+#pragma unroll 1
+    for (;;) {
+        const int un = u + stride;
+        NextW<kWT> nx;
+        nx.has = un < hi;
+        const BigItem itn = nx.has ? walk_unit(p, nb, un) : it;
+        {
+            int tid = threadIdx.x;
+            asm volatile("" : "+v"(tid));
+            nx.wt = l2_tiles<W>(p, itn, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63);
+        }
+        // items of at most 16 * kWalkMaxTiles rows (the host launches the walk
+        // only for such M tiles)
+        const int tiles = (it.rows + 15) >> 4;
+        switch (tiles) {
+#define MM_WALK_BODY(n) \
+    case n: l2_walk_body<W, n>(p, it, sm, ring, nx, pref); break;
+            MM_WALK_BODY(1) MM_WALK_BODY(2) MM_WALK_BODY(3) MM_WALK_BODY(4)
+            MM_WALK_BODY(5) MM_WALK_BODY(6) MM_WALK_BODY(7) default: MM_WALK_BODY(8)
+#undef MM_WALK_BODY
+        }
+        pref = nx.has ? kWalkStages - 1 : 0;
+        if (un >= hi) break;
+        __syncthreads();   // the next unit's staging reuses the LDS
+        u = un;
+        it = itn;
+    }
+}
+
+__global__ void __launch_bounds__(512) l2_walk_kernel(GemmParams p) {
+    __shared__ BigSmem sm;
+    if (!walk_taken(p)) return;   // l2_big_kernel, launched next, runs the units
+    l2_walk<8>(p, sm, blockIdx.x, gridDim.x);
 }
 
 // L1 and L2 in one launch: workgroups [0, g1) run L1 units, the rest L2

@@ -178,6 +178,21 @@ mm::GemmParams gemm_params(const MegaLaunchArgs& a, const Bound& b) {
 
 using GemmKernel = void (*)(mm::GemmParams);
 
+// Compute units of the current device (the L2 walk runs one workgroup on each).
+int cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 // Decode-shaped kernels (MT = 1, 2) for m_tile <= 32; above, the LDS-staged
 // kernels on a 1-D grid of nb * max_items + 8 workgroups (the kernel maps
 // workgroups to (item, block) units XCD by XCD and drops the surplus).
@@ -227,6 +242,17 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     p.xcd_cuts = p.status + mm::kCutsL2;
     p.queue = at<int>(b, b.L.status) + mm::kQueueL2;
     const int nb = a.hidden / mm::kL2BlockN;
+    // The walk and the one-unit kernel back to back: the device picks one of
+    // them from the routing of this launch (mm::walk_taken).  Not tried below
+    // 16 routed rows per expert on average, where items of more than 32 rows
+    // are rare and the walk's empty launch would cost ~3 us (T = 512).
+    // Measured on MI355X, walk on vs off: T = 2048 layer 1819-1820 vs
+    // 1846-1847 us (L2 613 vs 645-646); Zipf(1.1) T = 2048 and T = 8192 even
+    // (the one-unit kernel runs them).
+    if (b.m_tile > 32 && !a.l2_no_walk && (int64_t)a.tokens * a.topk > 16LL * a.num_experts) {
+        p.walk = 1;
+        hipLaunchKernelGGL(mm::l2_walk_kernel, dim3(cu_count()), dim3(mm::kBigThreads), 0, s, p);
+    }
     launch_gemm(kL2Small, mm::l2_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
 }
@@ -521,6 +547,7 @@ void dump_kernel_resources() {
     print_attr("l2_kernel<1>", (const void*)mm::l2_kernel<1>);
     print_attr("l2_kernel<2>", (const void*)mm::l2_kernel<2>);
     print_attr("l2_big_kernel", (const void*)mm::l2_big_kernel);
+    print_attr("l2_walk_kernel", (const void*)mm::l2_walk_kernel);
     print_attr("gemm_fused_kernel", (const void*)mm::gemm_fused_kernel);
     print_attr("combine", (const void*)mm::combine_kernel);
     std::fflush(stdout);
@@ -548,7 +575,7 @@ using fp8mega::MegaLaunchArgs;
 
 extern "C" {
 
-int mm_abi_version(void) { return 2; }
+int mm_abi_version(void) { return 3; }
 
 long long mm_noalloc_scratch_bytes(void) { return (long long)fp8mega::kScratchBytes; }
 
@@ -565,6 +592,7 @@ long long mm_args_offset(const char* f) {
     MM_FIELD(hidden) MM_FIELD(intermediate) MM_FIELD(max_tokens) MM_FIELD(workspace_bytes)
     MM_FIELD(x_sf) MM_FIELD(w1_sf) MM_FIELD(w2_sf) MM_FIELD(ffn_ue8m0) MM_FIELD(y_bf16)
     MM_FIELD(fuse_l1l2)
+    MM_FIELD(l2_no_walk)
 #undef MM_FIELD
     return -1;
 }

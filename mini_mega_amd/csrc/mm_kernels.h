@@ -32,6 +32,7 @@ constexpr int kStatusInts = 64;     // workspace status words
 constexpr int kStatusItemOverflow = fp8mega::kStatusItemOverflow;
 constexpr int kStatusWaitTimeout = fp8mega::kStatusWaitTimeout;
 constexpr int kReadySpinLimit = 1 << 20;   // default polls (~1 s with the sleep between)
+constexpr int kStatusMaxRows = 5;   // status[5]: rows of the largest work item
 constexpr int kCutsL1 = 16;         // status[16..24]: XCD unit ranges of the L1 big GEMM
 constexpr int kCutsL2 = 32;         // status[32..40]: the same for L2
 // Tail queues of the big GEMMs: per XCD a ticket counter over the last
@@ -70,12 +71,28 @@ struct GemmParams {
     int ready_target;         // L1 blocks per item (L2 waits for this count)
     int spin_limit;           // L2: polls of a ready counter before giving up
     int* err;                 // status word [0]: kStatusWaitTimeout on give-up
+    // L2 launched as the walk plus the one-unit-per-workgroup kernel: exactly
+    // one of the two runs the units (walk_taken decides from the item size)
+    int walk;
 };
+
+// The L2 walk takes the launch when its largest work item has 3..8 token tiles
+// and K / 128 is a multiple of its weight stages: its bodies hold at most 8
+// tiles (the weight ring stays live across units), and at 1-2 tiles the
+// one-unit kernel's six weight stages stream faster.
+constexpr int kWalkMaxTiles = 8;
+constexpr int kWalkStages = 4;     // weight stages of the walk; must divide K / 128
+__device__ __forceinline__ bool walk_taken(const GemmParams& p) {
+    if (!p.walk) return false;
+    const int rows = p.status[kStatusMaxRows];
+    return rows > 32 && rows <= 16 * kWalkMaxTiles && (p.I >> 7) % kWalkStages == 0;
+}
 
 template <int MT> __global__ void l1_kernel(GemmParams p);
 template <int MT> __global__ void l2_kernel(GemmParams p);
 __global__ void l1_big_kernel(GemmParams p);
 __global__ void l2_big_kernel(GemmParams p);
+__global__ void l2_walk_kernel(GemmParams p);
 __global__ void gemm_fused_kernel(GemmParams p1, GemmParams p2, int g1);
 
 __global__ void route_hist_kernel(const int64_t*, int, int, int, int*);

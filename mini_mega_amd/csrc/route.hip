@@ -71,9 +71,13 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     __shared__ int smem[kScanThreads / 64 + 1];
     __shared__ int cut_s[2][8];
     __shared__ int lh[kFusedHist];   // [chunk][expert] when topk_idx is given
+    __shared__ int s_rows;           // rows of the largest work item
     // the status word of this launch (only this kernel sets its error bits;
     // thread 0 clears it before its own atomicOr below)
-    if (threadIdx.x == 0) status[0] = 0;
+    if (threadIdx.x == 0) {
+        status[0] = 0;
+        s_rows = 0;
+    }
     // Small launches (topk_idx given, nchunks * E <= kFusedHist): the chunk
     // histograms of route_hist_kernel, built here in LDS, 8 pairs' loads in
     // flight per thread.
@@ -140,6 +144,7 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     // needs no offsets[] load after its item.
     const int nm = (cnt + m_tile - 1) / m_tile;
     const int sz = nm > 0 ? (cnt + nm - 1) / nm : 0;
+    if (sz > 0) atomicMax(&s_rows, sz);   // ordered before the read by the scan's barriers
     int nitems = 0;
     const int ioff = block_exclusive_scan(nm, smem, &nitems);
     for (int j = 0; j < nm; ++j) {
@@ -158,6 +163,7 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
         status[2] = slots;
         status[3] = valid - slots;   // pairs dropped by the slot capacity
         status[4] = P - valid;       // pairs whose expert id is outside [0, E)
+        status[kStatusMaxRows] = s_rows;
         if (nitems > max_items) atomicOr(&status[0], kStatusItemOverflow);
     }
     // XCD ranges of the big GEMMs' units (nb blocks per item; an expert's

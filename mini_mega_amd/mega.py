@@ -132,6 +132,9 @@ class SymmBuffer:
         # L1 and L2 in one launch, L2 units starting on an item once its L1
         # units are done (MegaLaunchArgs::fuse_l1l2)
         self.fuse_l1l2 = False
+        # L2 as a walk of one workgroup per CU where the items allow it
+        # (MegaLaunchArgs::l2_no_walk = 0)
+        self.l2_walk = True
         self.launch_count = 0
 
     # -- workspace views (staged parity checks read these, as check.cu dumps
@@ -199,6 +202,7 @@ class SymmBuffer:
         a.y_bf16 = y_bf16.data_ptr() if y_bf16 is not None else None
         a.skip_prologue = int(skip_prologue)
         a.fuse_l1l2 = int(bool(self.fuse_l1l2))
+        a.l2_no_walk = int(not self.l2_walk)
         a.num_experts, a.topk = self.num_experts, self.num_topk
         a.hidden, a.intermediate = self.hidden, self.intermediate_hidden
         a.max_tokens = self.num_max_tokens_per_rank
@@ -236,16 +240,18 @@ class SymmBuffer:
     def device_status(self) -> dict:
         """The device status words of the last launch on this buffer (through
         mm_read_status, which synchronises the current stream): error bits,
-        work items, routed slots, pairs dropped by the slot capacity and pairs
-        with an expert id outside [0, num_experts)."""
+        work items, routed slots, pairs dropped by the slot capacity, pairs
+        with an expert id outside [0, num_experts) and the rows of the largest
+        work item."""
         import ctypes as _c
         a = self.make_reduce_args(0, self.workspace)
-        out = (_c.c_int * 5)()
-        rc = lib().mm_read_status(_c.byref(a), out, 5, _stream_ptr())
+        out = (_c.c_int * 6)()
+        rc = lib().mm_read_status(_c.byref(a), out, 6, _stream_ptr())
         if rc not in (0, _lib.ERR_DEVICE):
             check("mm_read_status", rc)
         return dict(error=int(out[0]), items=int(out[1]), slots=int(out[2]),
-                    dropped_by_capacity=int(out[3]), invalid_ids=int(out[4]))
+                    dropped_by_capacity=int(out[3]), invalid_ids=int(out[4]),
+                    max_item_rows=int(out[5]))
 
     def destroy(self):
         self.buffer = self.workspace = self._y_fp32 = None

@@ -288,6 +288,49 @@ def test_fused_l1l2_matches_two_launches(E, K, H, I, T, zipf, win, scaled):
     buf.destroy()
 
 
+@pytest.mark.parametrize("E,K,H,I,T,zipf,win,scaled,walks", [
+    (32, 8, 1024, 512, 300, None, 0, True, True),
+    (32, 8, 1024, 512, 300, None, 0, False, True),
+    (48, 8, 1024, 1024, 600, 1.1, 128, True, True),
+    (64, 4, 2048, 768, 200, 1.1, 64, True, False),
+    (256, 8, 6144, 2048, 512, None, 0, True, False),
+    (256, 8, 6144, 2048, 2048, None, 0, True, True),
+])
+def test_l2_walk_matches_one_unit_kernel(E, K, H, I, T, zipf, win, scaled, walks):
+    """The L2 walk (one workgroup per CU, the next unit's weights streamed during
+    the current one) runs when the largest work item has 3..8 token tiles and
+    I / 128 is a multiple of 4 (the host tries it above 16 routed rows per
+    expert on average); otherwise the one-unit-per-workgroup kernel launched
+    after it does.  y, the ffn bytes and the L2 rows are bit-identical with the
+    walk disabled (l2_no_walk), including split experts (a 128-row window under
+    skew) and the raw path."""
+    _say(f"L2 walk E={E} T={T} zipf={zipf} win={win} scaled={scaled}")
+    c = mc.normal_case(E, K, H, I, T, seed=T + 11, scaled=scaled, zipf=zipf, win=win)
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I, expert_window=win)
+    _load(buf, c)
+    l1 = (c.w1, c.s1) if scaled else c.w1
+    l2 = (c.w2, c.s2) if scaled else c.w2
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    buf.l2_walk = False
+    mm.fp8_mega_moe(y, l1, l2, buf)
+    torch.cuda.synchronize()
+    want = _outputs(buf, c, y)
+    st = buf.device_status()
+    rows = st["max_item_rows"]
+    assert st["error"] == 0 and rows > 0
+    assert (32 < rows <= 128 and (I // 128) % 4 == 0) == walks, f"max item rows {rows}"
+    buf.l2_walk = True
+    for rep in range(2):
+        y.zero_()
+        buf.workspace[int(buf.layout.ffn):].zero_()
+        mm.fp8_mega_moe(y, l1, l2, buf)
+        torch.cuda.synchronize()
+        got = _outputs(buf, c, y)
+        for g, w, name in zip(got, want, ("y", "ffn", "l2")):
+            assert np.array_equal(g, w), f"walk launch {rep}: {name} differs"
+    assert buf.device_status()["error"] == 0
+
+
 def test_fused_l1l2_bounded_wait_reports_timeout():
     """With max_spins = 1 an L2 unit polls its item's ready counter once: the
     launch still ends (every wait is bounded), and a unit that gave up sets
