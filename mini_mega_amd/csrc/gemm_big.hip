@@ -695,6 +695,44 @@ __global__ void __launch_bounds__(512) l1_big_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------- L2 --
+// L2 epilogue: the unit's bf16 tile (rows x 256 channels) goes through LDS so
+// that every global store writes whole rows (a wave: two 512-byte rows per
+// instruction) instead of 32-byte pieces of 16 rows from the MFMA layout.
+// The caller's main loop ended on a barrier; the tile (<= 256 rows at a
+// 544-byte pitch, 136 KiB) overlays the LDS operand tiles and the scales.
+constexpr int kL2TilePitch = kL2BlockN * 2 + 32;
+static_assert(kBigRows * kL2TilePitch <= (int)sizeof(BigSmem), "L2 store tile");
+template <int W, int NT>
+__device__ __forceinline__ void l2_store_tile(const GemmParams& p, const BigItem& it, BigSmem& sm,
+                                              v4f (&acc)[Geo<W>::kWT][NT], int c0, int lane,
+                                              int wave) {
+    constexpr int kWT = Geo<W>::kWT;
+    uint8_t* tile = reinterpret_cast<uint8_t*>(&sm);
+    // channel 32w + 16t + 4(L/16) + i, row 16j + L%16 (the MFMA output layout)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int t = 0; t < kWT; ++t) {
+            uint2 v;
+            v.x = pack2_bf16(acc[t][j][0], acc[t][j][1]);
+            v.y = pack2_bf16(acc[t][j][2], acc[t][j][3]);
+            const int r = 16 * j + (lane & 15);
+            const int c = wave * (kL2BlockN / W) + 16 * t + 4 * (lane >> 4);
+            *reinterpret_cast<uint2*>(tile + r * kL2TilePitch + c * 2) = v;
+        }
+    __syncthreads();
+    // 16 rows per pass: thread T copies 16 bytes (8 channels) of row T / 32
+    constexpr int kThreads = Geo<W>::kThreads;
+    const int tid = wave * 64 + lane;
+#pragma unroll
+    for (int pass = 0; pass < NT * 16 * 32 / kThreads; ++pass) {
+        const int i = pass * kThreads + tid, r = i >> 5, ch = (i & 31) * 8;
+        if (r < it.rows)
+            *reinterpret_cast<v4i*>(p.out16 + (size_t)(it.m0 + r) * p.H + c0 + ch) =
+                *reinterpret_cast<const v4i*>(tile + r * kL2TilePitch + ch * 2);
+    }
+}
+
 // kFused: the item's ffn rows come from L1 units of the same launch, read at
 // device scope (the caller's stage_scales waits for them first).
 template <int W, int NT, bool kFused, class ScalesF>
@@ -721,20 +759,7 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     });
     v4f acc[kWT][NT];
     big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const int r = 16 * j + (lane & 15);
-        if (r < it.rows) {
-            uint16_t* dst = p.out16 + (size_t)(it.m0 + r) * H + n0 + 4 * (lane >> 4);
-#pragma unroll
-            for (int t = 0; t < kWT; ++t) {
-                uint2 v;
-                v.x = pack2_bf16(acc[t][j][0], acc[t][j][1]);
-                v.y = pack2_bf16(acc[t][j][2], acc[t][j][3]);
-                *reinterpret_cast<uint2*>(dst + 16 * t) = v;
-            }
-        }
-    }
+    l2_store_tile<W, NT>(p, it, sm, acc, it.bx * kL2BlockN, lane, wave);
 }
 
 // Workgroup L of the `grid` L2 workgroups.  kFused: before reading the
@@ -864,20 +889,7 @@ __device__ __forceinline__ void l2_walk_body(const GemmParams& p, const BigItem&
     v4f acc[kWT][NT];
     big_mainloop<W, NT, S, false>(acc, sm, xl, wt, KT, ring, nx, pref);
     const int n0 = it.bx * kL2BlockN + wave * (kL2BlockN / W);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const int r = 16 * j + (lane & 15);
-        if (r < it.rows) {
-            uint16_t* dst = p.out16 + (size_t)(it.m0 + r) * H + n0 + 4 * (lane >> 4);
-#pragma unroll
-            for (int t = 0; t < kWT; ++t) {
-                uint2 v;
-                v.x = pack2_bf16(acc[t][j][0], acc[t][j][1]);
-                v.y = pack2_bf16(acc[t][j][2], acc[t][j][3]);
-                *reinterpret_cast<uint2*>(dst + 16 * t) = v;
-            }
-        }
-    }
+    l2_store_tile<W, NT>(p, it, sm, acc, it.bx * kL2BlockN, lane, wave);
 }
 
 template <int W>
