@@ -396,9 +396,12 @@ struct BigItem {
 // at T = 8192 and 120 us with Zipf(1.1) skew; with it 22, 55 and 91 us.  A
 // stolen unit runs without the victim XCD's L2 contents, so the kernel span
 // shrinks less than the spread: L1 with Zipf(1.1) T = 2048 1260 -> 1216 us,
-// T = 8192 -9 us, T = 512 and 2048 even.  L2's units are a third as long,
-// and there the queue cost 6-10 us at T = 512 and 2048, so only L1 uses it
-// (big_unit<true>); L2 runs each range statically.
+// T = 8192 -9 us, T = 512 and 2048 even.  L2's units are a third as long:
+// there the queue cost 6-10 us at T = 512 and 2048 (items of 1-4 token
+// tiles), and saved 2-4% of L2 at T = 8192 (1571-1586 vs 1603-1612 us) and
+// with Zipf(1.1) skew at T = 2048 (651-663 vs 678-679 us), so L2 takes
+// tickets only when its largest item has more than 32 rows (at T = 2048 the
+// walk runs those launches).
 __device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool own, int grid) {
     int u = -1;
     for (int d = own ? 0 : 1; d < 8 && u < 0; ++d) {
@@ -771,7 +774,12 @@ template <int W, bool kFused>
 __device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_unit, int L,
                                        int grid) {
     BigItem it;
-    if (!big_unit<false>(p, p.H / kL2BlockN, it, s_unit, L, grid)) return;
+    // the tail queue for items of more than 32 rows (at 1-2 token tiles the
+    // units are short and the tickets cost more than they balance)
+    const bool tail = !kFused && p.status[kStatusMaxRows] > 32;
+    if (tail ? !big_unit<true>(p, p.H / kL2BlockN, it, s_unit, L, grid)
+             : !big_unit<false>(p, p.H / kL2BlockN, it, s_unit, L, grid))
+        return;
     const int KT = p.I >> 7, H = p.H;
     const int tiles = (it.rows + 15) >> 4;
     // scales: ffn rows in slot order; W2 tiles of this block's 256 channels

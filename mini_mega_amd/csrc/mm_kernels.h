@@ -38,8 +38,9 @@ constexpr int kCutsL2 = 32;         // status[32..40]: the same for L2
 // Tail queues of the big GEMMs: per XCD a ticket counter over the last
 // kQueueTail units of its range, plus a count of the workgroups that took
 // tickets (status[44..52] for L1, [53..61] for L2; zeroed by the routing
-// scan and again by the last ticket taker of each launch).  Only L1 takes
-// tickets (gemm_big.hip: big_unit<true>); L2's counters stay zero.
+// scan and again by the last ticket taker of each launch).  L1 always takes
+// tickets, L2 when its largest item has more than 32 rows (gemm_big.hip:
+// big_unit<true>).
 constexpr int kQueueInts = 9;
 constexpr int kQueueL1 = 44;
 constexpr int kQueueL2 = kQueueL1 + kQueueInts;
