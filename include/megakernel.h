@@ -130,8 +130,9 @@ struct MegaLaunchArgs {
                                            // 1948-1997).  Windows > 32 rows; max_spins > 0
                                            // bounds each wait (else ~1 s).
     int l2_no_walk = 0;                    // 1: L2 always one unit per workgroup; 0: when the
-                                           // largest work item has 3-8 token tiles, one
-                                           // workgroup per CU walks the units, streaming
+                                           // largest work item has 3-8 token tiles (tried
+                                           // for 17-128 routed rows per expert on average),
+                                           // one workgroup per CU walks the units, streaming
                                            // the next unit's weights during the current one
 };
 

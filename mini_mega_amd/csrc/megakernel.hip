@@ -243,13 +243,17 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     p.queue = at<int>(b, b.L.status) + mm::kQueueL2;
     const int nb = a.hidden / mm::kL2BlockN;
     // The walk and the one-unit kernel back to back: the device picks one of
-    // them from the routing of this launch (mm::walk_taken).  Not tried below
-    // 16 routed rows per expert on average, where items of more than 32 rows
-    // are rare and the walk's empty launch would cost ~3 us (T = 512).
+    // them from the routing of this launch (mm::walk_taken).  Tried for 17 to
+    // 128 routed rows per expert on average: below, items of more than 32
+    // rows are rare; above, items of at most 128 rows are (T = 8192); there
+    // the empty launch would only cost time (~5 us for the walk's, ~7 us for
+    // the one-unit kernel's, measured).
     // Measured on MI355X, walk on vs off: T = 2048 layer 1819-1820 vs
     // 1846-1847 us (L2 613 vs 645-646); Zipf(1.1) T = 2048 and T = 8192 even
     // (the one-unit kernel runs them).
-    if (b.m_tile > 32 && !a.l2_no_walk && (int64_t)a.tokens * a.topk > 16LL * a.num_experts) {
+    const int64_t pairs = (int64_t)a.tokens * a.topk;
+    if (b.m_tile > 32 && !a.l2_no_walk && pairs > 16LL * a.num_experts &&
+        pairs <= 128LL * a.num_experts) {
         p.walk = 1;
         hipLaunchKernelGGL(mm::l2_walk_kernel, dim3(cu_count()), dim3(mm::kBigThreads), 0, s, p);
     }
