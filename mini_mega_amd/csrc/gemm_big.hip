@@ -822,12 +822,15 @@ __global__ void __launch_bounds__(512) l2_big_kernel(GemmParams p) {
 
 // ------------------------------------------------------------- L2 walker --
 // One workgroup per CU walks its XCD's unit range at a stride of the XCD's
-// workgroup count.  A unit's last k-steps issue the next unit's first weight
-// stages (NextW), so the CU's weight stream does not drain at the unit
-// boundary: the next unit's scale staging and first activation commit wait for
-// loads that were issued during the previous unit, and no workgroup is
-// dispatched in between.  Weight stages: 4 up to 12 token tiles, 2 above (both
-// divide K / 128 = 16 k-steps, so the ring's slots line up across units).
+// workgroup count (the same units in flight as with one unit per workgroup).
+// A unit's last k-steps issue the next unit's first weight stages (NextW), so
+// the CU's weight stream does not drain at the unit boundary: the next unit's
+// scale staging and first activation commit wait for loads that were issued
+// during the previous unit, its epilogue overlaps them, and no workgroup is
+// dispatched in between.  kWalkStages (4) weight stages divide K / 128 = 16,
+// so the ring's slots line up across units; the ring stays live across the
+// walk, which therefore holds bodies of at most kWalkMaxTiles token tiles
+// (with the larger ones the compiler spilled 250-600 VGPRs).
 
 // (item, block) of unit u, as big_unit decodes it.
 __device__ __forceinline__ BigItem walk_unit(const GemmParams& p, int nb, int u) {
@@ -860,11 +863,10 @@ __device__ __forceinline__ WTiles<Geo<W>::kWT> l2_tiles(const GemmParams& p, con
 }
 
 
-// One unit of the walk.  w: the weight ring (4 stages; bodies of 2 stages use
-// its first two); pref: stages of this unit the previous one issued; nx: the
-// next unit.  The thread index goes through an empty asm once per unit, so that
+// One unit of the walk.  ring: the kWalkStages weight stages; pref: stages of
+// this unit the previous one issued; nx: the next unit.  The thread index goes through an empty asm once per unit, so that
 // the optimiser does not hoist every body's thread-index arithmetic out of the
-// walk (where it stays live across all sixteen bodies and spills).
+// walk (where it stays live across all the bodies and spills).
 template <int W, int NT>
 __device__ __forceinline__ void l2_walk_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
                                              WStage<Geo<W>::kWT> (&ring)[4],
@@ -922,8 +924,7 @@ __device__ __forceinline__ void l2_walk(const GemmParams& p, BigSmem& sm, int L,
             asm volatile("" : "+v"(tid));
             nx.wt = l2_tiles<W>(p, itn, __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63);
         }
-        // items of at most 16 * kWalkMaxTiles rows (the host launches the walk
-        // only for such M tiles)
+        // items of at most 16 * kWalkMaxTiles rows (walk_taken)
         const int tiles = (it.rows + 15) >> 4;
         switch (tiles) {
 #define MM_WALK_BODY(n) \
