@@ -864,9 +864,10 @@ __device__ __forceinline__ WTiles<Geo<W>::kWT> l2_tiles(const GemmParams& p, con
 
 
 // One unit of the walk.  ring: the kWalkStages weight stages; pref: stages of
-// this unit the previous one issued; nx: the next unit.  The thread index goes through an empty asm once per unit, so that
-// the optimiser does not hoist every body's thread-index arithmetic out of the
-// walk (where it stays live across all the bodies and spills).
+// this unit the previous one issued; nx: the next unit.  The thread index
+// goes through an empty asm once per unit, so that the optimiser does not
+// hoist every body's thread-index arithmetic out of the walk (where it stays
+// live across all the bodies and spills).
 template <int W, int NT>
 __device__ __forceinline__ void l2_walk_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
                                              WStage<Geo<W>::kWT> (&ring)[4],
