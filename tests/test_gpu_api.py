@@ -303,7 +303,7 @@ def test_l2_walk_matches_one_unit_kernel(E, K, H, I, T, zipf, win, scaled, walks
     expert on average); otherwise the one-unit-per-workgroup kernel launched
     after it does.  y, the ffn bytes and the L2 rows are bit-identical with the
     walk disabled (l2_no_walk), including split experts (a 128-row window under
-    skew) and the raw path."""
+    skew) and the raw path; a graph of two launches replays to the same y."""
     _say(f"L2 walk E={E} T={T} zipf={zipf} win={win} scaled={scaled}")
     c = mc.normal_case(E, K, H, I, T, seed=T + 11, scaled=scaled, zipf=zipf, win=win)
     buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I, expert_window=win)
@@ -329,6 +329,24 @@ def test_l2_walk_matches_one_unit_kernel(E, K, H, I, T, zipf, win, scaled, walks
         for g, w, name in zip(got, want, ("y", "ffn", "l2")):
             assert np.array_equal(g, w), f"walk launch {rep}: {name} differs"
     assert buf.device_status()["error"] == 0
+    # two launches (walk and one-unit kernel each) as one graph, replayed twice
+    ys = [torch.empty((T, H), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for yy in ys:
+                mm.fp8_mega_moe(yy, l1, l2, buf)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(2):
+        for yy in ys:
+            yy.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for yy in ys:
+            assert np.array_equal(yy.view(torch.int16).cpu().numpy(), want[0]), \
+                f"walk graph replay {rep} differs"
 
 
 def test_fused_l1l2_bounded_wait_reports_timeout():
