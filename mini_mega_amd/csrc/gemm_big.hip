@@ -899,7 +899,6 @@ __device__ __forceinline__ void l2_walk_body(const GemmParams& p, const BigItem&
     });
     v4f acc[kWT][NT];
     big_mainloop<W, NT, S, false>(acc, sm, xl, wt, KT, ring, nx, pref);
-    const int n0 = it.bx * kL2BlockN + wave * (kL2BlockN / W);
     l2_store_tile<W, NT>(p, it, sm, acc, it.bx * kL2BlockN, lane, wave);
 }
 
