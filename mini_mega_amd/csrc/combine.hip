@@ -9,11 +9,16 @@
 // k-loop runs in groups of 8 whose slot indices, weights and row loads are
 // all issued before the group's in-order accumulation, so a thread waits for
 // one memory latency per group instead of one per k.
+// One workgroup covers a token's H channels when H / 8 <= 1024 threads.  The
+// outputs are stored non-temporally (nothing in the layer reads them back);
+// the L2 rows are loaded non-temporally when kStreamRows, which the host
+// picks when they exceed the Infinity Cache (measured on MI355X below).
 #include "mm_kernels.h"
 
 namespace mm {
 
-__global__ void __launch_bounds__(256)
+template <bool kStreamRows>
+__global__ void __launch_bounds__(1024)
 combine_kernel(const uint16_t* __restrict__ l2, const int* __restrict__ pair_pos,
                const float* __restrict__ w, int topk, int H, float* __restrict__ y,
                uint16_t* __restrict__ y_bf16) {
@@ -38,9 +43,12 @@ combine_kernel(const uint16_t* __restrict__ l2, const int* __restrict__ pair_pos
         }
 #pragma unroll
         for (int j = 0; j < kG; ++j)
-            raw[j] = pos[j] >= 0
-                         ? load16(reinterpret_cast<const uint8_t*>(l2 + (size_t)pos[j] * H + c0))
-                         : v4i{0, 0, 0, 0};
+        {
+            const uint8_t* row = reinterpret_cast<const uint8_t*>(l2 + (size_t)pos[j] * H + c0);
+            raw[j] = pos[j] < 0   ? v4i{0, 0, 0, 0}
+                     : kStreamRows ? load16_stream(row)
+                                   : load16(row);
+        }
 #pragma unroll
         for (int j = 0; j < kG; ++j) {
             if (pos[j] < 0) continue;
@@ -55,17 +63,22 @@ combine_kernel(const uint16_t* __restrict__ l2, const int* __restrict__ pair_pos
         }
     }
     if (y) {
-        float4* yo = reinterpret_cast<float4*>(y + (size_t)t * H + c0);
-        yo[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        yo[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        v4f* yo = reinterpret_cast<v4f*>(y + (size_t)t * H + c0);
+        __builtin_nontemporal_store(v4f{acc[0], acc[1], acc[2], acc[3]}, yo);
+        __builtin_nontemporal_store(v4f{acc[4], acc[5], acc[6], acc[7]}, yo + 1);
     }
     if (y_bf16) {
         v4i o;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             o[i] = (int)(bf16_rne(acc[2 * i]) | (bf16_rne(acc[2 * i + 1]) << 16));
-        *reinterpret_cast<v4i*>(y_bf16 + (size_t)t * H + c0) = o;
+        __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(y_bf16 + (size_t)t * H + c0));
     }
 }
+
+template __global__ void combine_kernel<false>(const uint16_t*, const int*, const float*, int, int,
+                                               float*, uint16_t*);
+template __global__ void combine_kernel<true>(const uint16_t*, const int*, const float*, int, int,
+                                              float*, uint16_t*);
 
 }  // namespace mm

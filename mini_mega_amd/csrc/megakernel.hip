@@ -255,7 +255,9 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     if (b.m_tile > 32 && !a.l2_no_walk && pairs > 16LL * a.num_experts &&
         pairs <= 128LL * a.num_experts) {
         p.walk = 1;
-        hipLaunchKernelGGL(mm::l2_walk_kernel, dim3(cu_count()), dim3(mm::kBigThreads), 0, s, p);
+        // at least one workgroup per XCD range (workgroup L walks range L % 8)
+        const int walkers = cu_count() < 8 ? 8 : cu_count();
+        hipLaunchKernelGGL(mm::l2_walk_kernel, dim3(walkers), dim3(mm::kBigThreads), 0, s, p);
     }
     launch_gemm(kL2Small, mm::l2_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
@@ -269,10 +271,20 @@ int do_reduce(const MegaLaunchArgs& a, hipStream_t s) {
     // has a null data pointer)
     if (a.skip_combine || a.tokens == 0) return kOk;
     if (a.y == nullptr && a.y_bf16 == nullptr) return kErrNullPointer;
-    const int per_block = 256 * 8;
+    // a token per workgroup (H / 8 threads, whole waves) up to 1024 threads
+    const int threads = a.hidden / 8 <= 1024 ? (a.hidden / 8 + 63) / 64 * 64 : 256;
+    const int per_block = threads * 8;
     const dim3 grid(a.tokens, (a.hidden + per_block - 1) / per_block);
-    hipLaunchKernelGGL(mm::combine_kernel, grid, dim3(256), 0, s, at<uint16_t>(b, b.L.l2),
-                       at<int>(b, b.L.pair_pos), b.w, a.topk, a.hidden, a.y, a.y_bf16);
+    // The L2 rows stream past the caches once they are well over the 256 MiB
+    // Infinity Cache; smaller ones are still cached from L2's stores.  Measured
+    // on MI355X (combine us, cached vs streamed loads, streamed stores both):
+    // T = 2048 (192 MiB of rows) 34.4 vs 37.0, T = 3072 52.2 vs 57.9,
+    // T = 4096 86.6 vs 77.3, T = 8192 171.6 vs 155.5 (before: 34.8, 61.8,
+    // 93, 183 with 256-thread blocks and cached stores).
+    const bool stream_rows = 2LL * a.tokens * a.topk * a.hidden >= (384LL << 20);
+    hipLaunchKernelGGL(stream_rows ? mm::combine_kernel<true> : mm::combine_kernel<false>, grid,
+                       dim3(threads), 0, s, at<uint16_t>(b, b.L.l2), at<int>(b, b.L.pair_pos), b.w,
+                       a.topk, a.hidden, a.y, a.y_bf16);
     return launched(kOk);
 }
 
@@ -553,7 +565,8 @@ void dump_kernel_resources() {
     print_attr("l2_big_kernel", (const void*)mm::l2_big_kernel);
     print_attr("l2_walk_kernel", (const void*)mm::l2_walk_kernel);
     print_attr("gemm_fused_kernel", (const void*)mm::gemm_fused_kernel);
-    print_attr("combine", (const void*)mm::combine_kernel);
+    print_attr("combine<cached rows>", (const void*)mm::combine_kernel<false>);
+    print_attr("combine<streamed rows>", (const void*)mm::combine_kernel<true>);
     std::fflush(stdout);
 }
 

@@ -103,6 +103,7 @@ __global__ void route_scatter_kernel(const int64_t*, int, int, int, int, const i
                                      const int*, uint32_t*, int*);
 __global__ void dispatch_gather_kernel(const uint8_t*, int, int, const uint32_t*, const int*,
                                        uint8_t*);
+template <bool kStreamRows>
 __global__ void combine_kernel(const uint16_t*, const int*, const float*, int, int, float*,
                                uint16_t*);
 __global__ void fill_w_lane_kernel(uint8_t*, int, int, uint32_t);
