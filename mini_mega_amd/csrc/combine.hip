@@ -12,7 +12,8 @@
 // One workgroup covers a token's H channels when H / 8 <= 1024 threads.  The
 // outputs are stored non-temporally (nothing in the layer reads them back);
 // the L2 rows are loaded non-temporally when kStreamRows, which the host
-// picks when they exceed the Infinity Cache (measured on MI355X below).
+// picks when they exceed the Infinity Cache (do_reduce in megakernel.hip
+// holds the rule and its measurements).
 #include "mm_kernels.h"
 
 namespace mm {
