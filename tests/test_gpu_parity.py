@@ -445,11 +445,13 @@ def test_real_decode_routes_full_layer(launch):
 
 
 # ------------------------------------------------------------ full sizes --
-@pytest.mark.parametrize("T,zipf", [(512, None), (2048, None), (2048, 1.1), (8192, None)])
+@pytest.mark.parametrize("T,zipf", [(512, None), (2048, None), (2048, 1.1), (4096, None),
+                                    (8192, None)])
 def test_full_size_layer(T, zipf):
     """The benchmark workloads at full size: routing exact, staged L1/L2 on
     the busiest / a median / the lightest expert, REDUCE bit-exact, and the
-    whole chain on a token subset."""
+    whole chain on a token subset.  T=4096 puts exactly 384 MiB of L2 rows in
+    front of combine, the smallest size at which it streams them."""
     _say(f"full size T={T} zipf={zipf}")
     c = mc.normal_case(256, 8, 6144, 2048, T, seed=T + 1, scaled=True, zipf=zipf)
     r = mc.run_layer(c)
