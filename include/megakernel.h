@@ -66,6 +66,8 @@ enum MegaStatus : int {
 //   [4]  pairs whose expert id is outside [0, num_experts) (dropped)
 //   [5]  rows of the largest work item (the L2 walk runs when 33..128)
 //   [16..24], [32..40] the big GEMMs' XCD unit ranges (L1, L2)
+// (read_status returns these 64 words; the region's next 256 bytes hold the
+// L1 tail queues' ticket order, also written by the routing)
 // The reference returns no status (src/megakernel.h:117-130): its launches
 // are void and its host CHECKs exit (src/host_layout.cuh:18-26).
 enum MegaDeviceStatus : int {
@@ -140,8 +142,9 @@ struct MegaLaunchArgs {
 // counterpart of mt::make_geo / compute_layout, test/mega_common.cuh:69-88,
 // src/host_layout.cuh:59-100).  All offsets are 256-byte aligned.
 struct MegaLayout {
-    int64_t status;        // int32[64]: [0] status word, [1] items, [2] slots,
-                           // [16..24] / [32..40] XCD unit ranges of the L1 / L2 GEMMs
+    int64_t status;        // int32[128]: [0] status word, [1] items, [2] slots,
+                           // [16..24] / [32..40] XCD unit ranges of the L1 / L2 GEMMs;
+                           // bytes [256..512): L1's tail-queue ticket order [8][32]
     int64_t chunk_hist;    // int32[nchunks][E] per-chunk histograms -> prefixes
     int64_t counts;        // int32[E]   per-expert routed rows (after cap)
     int64_t offsets;       // int32[E+1] exclusive prefix of counts

@@ -401,7 +401,12 @@ struct BigItem {
 // tiles), and saved 2-4% of L2 at T = 8192 (1571-1586 vs 1603-1612 us) and
 // with Zipf(1.1) skew at T = 2048 (651-663 vs 678-679 us), so L2 takes
 // tickets only when its largest item has more than 32 rows (at T = 2048 the
-// walk runs those launches).
+// walk runs those launches).  L1's tickets go out costliest unit first (by
+// the token tiles of the unit's item; the order is the routing scan's
+// tail_ord), so that no heavy unit starts after the light ones of its tail:
+// Zipf(1.1) T = 2048 L1 1193-1195 vs 1223-1231 us, T = 512 / 2048 / 8192
+// even (measured on MI355X).  L2's tickets gained nothing from the order
+// and go out in unit order.
 __device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool own, int grid) {
     int u = -1;
     for (int d = own ? 0 : 1; d < 8 && u < 0; ++d) {
@@ -410,7 +415,7 @@ __device__ __forceinline__ int claim_tail_unit(const GemmParams& p, int x, bool 
         const int tail = min(hi - lo, kQueueTail);
         if (tail <= 0) continue;
         const int t = atomicAdd(&p.queue[xx], 1);
-        if (t < tail) u = hi - tail + t;
+        if (t < tail) u = hi - tail + (p.tail_ord ? p.tail_ord[kQueueTail * xx + t] : t);
     }
     // ticket takers of this launch: per XCD, its workgroups from the tail
     // through its stealers (as many as the grid holds)

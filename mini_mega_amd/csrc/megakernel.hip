@@ -223,6 +223,7 @@ int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     p.out_sf = b.ws + b.L.ffn_sf;
     p.xcd_cuts = p.status + mm::kCutsL1;
     p.queue = at<int>(b, b.L.status) + mm::kQueueL1;
+    p.tail_ord = reinterpret_cast<const uint8_t*>(p.status + mm::kTailOrdL1);
     const int nb = a.intermediate / mm::kL1BlockH;
     launch_gemm(kL1Small, mm::l1_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
     return launched(kOk);
@@ -313,6 +314,7 @@ int do_l1_l2_fused(const MegaLaunchArgs& a, hipStream_t s) {
     p1.out_sf = b.ws + b.L.ffn_sf;
     p1.xcd_cuts = p1.status + mm::kCutsL1;
     p1.queue = at<int>(b, b.L.status) + mm::kQueueL1;
+    p1.tail_ord = reinterpret_cast<const uint8_t*>(p1.status + mm::kTailOrdL1);
     p2.x = b.ws + b.L.ffn;
     p2.x_sf = a.ffn_ue8m0 ? b.ws + b.L.ffn_sf : nullptr;
     p2.w = a.w2;
@@ -574,7 +576,7 @@ int last_error() { return g_last_error; }
 
 int read_status(const MegaLaunchArgs& a, int32_t* out, int n, hipStream_t s) {
     if (out == nullptr) return record(kErrNullPointer);
-    if (n < 1 || n > mm::kStatusInts) return record(kErrBadDims);
+    if (n < 1 || n > mm::kStatusWords) return record(kErrBadDims);
     Bound b;
     int st = bind(a, b, false);
     if (st != kOk) return record(st);

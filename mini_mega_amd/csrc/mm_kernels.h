@@ -28,7 +28,9 @@ constexpr int kBigMaxTiles = 16;    // large-M GEMMs: up to 16 token tiles (256 
 constexpr int kBigMaxKT = 64;       // large-M GEMMs: K / 128 <= 64 (H, I <= 8192)
 constexpr int kL1BlockH = 128;      // hidden columns (gate+up pairs) per L1 workgroup
 constexpr int kL2BlockN = 256;      // output channels per L2 workgroup
-constexpr int kStatusInts = 64;     // workspace status words
+constexpr int kStatusWords = 64;    // status words (readable with read_status)
+constexpr int kTailOrdL1 = 64;      // status[64..127] as bytes [8][kQueueTail]: L1 tail ticket order
+constexpr int kStatusInts = 128;    // the workspace's status region
 constexpr int kStatusItemOverflow = fp8mega::kStatusItemOverflow;
 constexpr int kStatusWaitTimeout = fp8mega::kStatusWaitTimeout;
 constexpr int kReadySpinLimit = 1 << 20;   // default polls (~1 s with the sleep between)
@@ -40,12 +42,14 @@ constexpr int kCutsL2 = 32;         // status[32..40]: the same for L2
 // tickets (status[44..52] for L1, [53..61] for L2; zeroed by the routing
 // scan and again by the last ticket taker of each launch).  L1 always takes
 // tickets, L2 when its largest item has more than 32 rows (gemm_big.hip:
-// big_unit<true>).
+// big_unit<true>).  L1's tickets go out costliest unit first: the routing
+// scan writes each tail's order (kTailOrdL1); L2's go out in unit order.
 constexpr int kQueueInts = 9;
 constexpr int kQueueL1 = 44;
 constexpr int kQueueL2 = kQueueL1 + kQueueInts;
 constexpr int kQueueTail = 32;      // units per XCD handed out by ticket (one per CU)
 constexpr int kStealers = 8;        // workgroups per XCD past its range that take others' tickets
+static_assert(kQueueTail * 8 <= (kStatusInts - kTailOrdL1) * 4, "the tail order fits");
 
 // Parameters of the two grouped GEMMs (one struct so that the launcher and
 // the kernels agree on one argument list).
@@ -61,6 +65,8 @@ struct GemmParams {
     const int* status;        // [1] = number of items
     const int* xcd_cuts;      // [9]: XCD x runs big-GEMM units [cuts[x], cuts[x+1])
     int* queue;               // [kQueueInts]: the tail queue of these units
+    const uint8_t* tail_ord;  // [8][kQueueTail]: ticket t of XCD x runs tail unit tail_ord[32x + t]
+                              // (null: tail unit t)
     const uint32_t* perm;     // slot -> pair (L1 gathers x rows through it)
     uint8_t* out8;            // L1: ffn fp8 [P][I]
     uint8_t* out_sf;          // L1: ffn scales [P][I/128] (ffn_ue8m0)

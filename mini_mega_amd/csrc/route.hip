@@ -7,7 +7,9 @@
 //   1. route_hist:    per chunk of pairs, an LDS histogram over experts.
 //   2. route_scan:    one workgroup; per expert the exclusive prefix over chunks,
 //                     the capped count, the exclusive prefix over experts
-//                     (slot offsets) and the work-item list (expert, first row).
+//                     (slot offsets), the work-item list (expert, first row),
+//                     the big GEMMs' XCD unit ranges and the ticket order
+//                     of L1's tail queues.
 //   3. route_scatter: per chunk, a stable rank of every pair among the pairs of
 //                     the same expert (wave ballots over the expert-id bits +
 //                     an LDS prefix across waves), giving the canonical slot
@@ -72,6 +74,10 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     __shared__ int cut_s[2][8];
     __shared__ int lh[kFusedHist];   // [chunk][expert] when topk_idx is given
     __shared__ int s_rows;           // rows of the largest work item
+    __shared__ int cuts_sh[9];       // the L1 XCD unit ranges
+    __shared__ int s_ioff[kMaxExperts + 1];     // first item of each expert (+ the item count)
+    __shared__ int s_cnt[kMaxExperts];          // routed rows of each expert
+    __shared__ uint8_t tnt[8][kQueueTail];      // token tiles of L1's tail units
     // the status word of this launch (only this kernel sets its error bits;
     // thread 0 clears it before its own atomicOr below)
     if (threadIdx.x == 0) {
@@ -204,9 +210,64 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
             v = min(max(v, prev), prev + cap);
             v = max(v, units - (8 - x) * cap);
             cuts[x] = v;
+            if (threadIdx.x == 0) cuts_sh[x] = v;
             prev = v;
         }
         cuts[8] = units;
+        if (threadIdx.x == 0) {
+            cuts_sh[0] = 0;
+            cuts_sh[8] = units;
+        }
+    }
+    // Ticket order of L1's tail queues (the last t = min(range, kQueueTail)
+    // units of each XCD range): costliest unit first, i.e. by the token tiles
+    // of its item, descending, ties in unit order, so that heavy units do not
+    // start after light ones at the end of the kernel.  Tail unit i of XCD x
+    // is unit cuts[x + 1] - t + i; L1 runs ticket k as tail unit order[k]
+    // (gemm_big.hip: claim_tail_unit).  One thread per tail slot finds its
+    // unit's expert by binary search over the item offsets.  When no item
+    // exceeds 32 rows (units of 1-2 tiles, about equal) the order is the
+    // identity and costs nothing.  (Measured on MI355X: a loop over the 8
+    // tails in every expert thread added 10.6 us to this one-workgroup
+    // kernel; L2's tails gained nothing from the order and keep ticket order.)
+    if (e < E) {
+        s_ioff[e] = ioff;
+        s_cnt[e] = cnt;
+    }
+    if (threadIdx.x == 0) s_ioff[E] = nitems;
+    __syncthreads();
+    const bool order_l1 = s_rows > 32;
+    if (threadIdx.x < 8 * kQueueTail) {
+        const int x = threadIdx.x / kQueueTail, i = threadIdx.x % kQueueTail;
+        const int lo = cuts_sh[x], hi = cuts_sh[x + 1], t = min(hi - lo, kQueueTail);
+        if (order_l1 && i < t) {
+            const int u = hi - t + i, im = u / nb1;
+            int a = 0, b = E - 1;   // the last expert whose first item is <= im
+            while (a < b) {
+                const int m = (a + b + 1) >> 1;
+                if (s_ioff[m] <= im) a = m; else b = m - 1;
+            }
+            const int n = max(s_ioff[a + 1] - s_ioff[a], 1), c = s_cnt[a];
+            const int z = (c + n - 1) / n, j = (u - nb1 * s_ioff[a]) % n;
+            tnt[x][i] = (uint8_t)min((min(c, (j + 1) * z) - j * z + 15) >> 4, kBigMaxTiles);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 8 * kQueueTail) {
+        const int x = threadIdx.x / kQueueTail, i = threadIdx.x % kQueueTail;
+        const int t = min(cuts_sh[x + 1] - cuts_sh[x], kQueueTail);
+        if (i < t) {
+            int r = i;
+            if (order_l1) {
+                const int v = tnt[x][i];
+                r = 0;
+                for (int k = 0; k < t; ++k) {
+                    const int w = tnt[x][k];
+                    r += (w > v) || (w == v && k < i);
+                }
+            }
+            reinterpret_cast<uint8_t*>(status + kTailOrdL1)[kQueueTail * x + r] = (uint8_t)i;
+        }
     }
 }
 

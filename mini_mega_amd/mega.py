@@ -167,6 +167,12 @@ class SymmBuffer:
     def status(self):
         return self._ws(self.layout.status, torch.int32, (64,))
 
+    def tail_orders(self):
+        """L1's tail-queue ticket order, uint8 [XCD][32]: ticket t of XCD x
+        runs the tail's unit [x][t] (the status region's bytes after its 64
+        words)."""
+        return self._ws(int(self.layout.status) + 256, torch.uint8, (8, 32))
+
     def items(self, n: int):
         """Work items: (expert, first slot, end slot, j | n << 16 for item j of
         the expert's n)."""

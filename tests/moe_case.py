@@ -167,6 +167,12 @@ def check_routing(c: Case, r: Run):
         cuts = np.asarray(r.status[base:base + 9]).astype(np.int64)
         assert np.array_equal(cuts, xcd_cuts(counts, m_tile, nb, max_items)), \
             f"XCD unit ranges differ (nb={nb})"
+        if base == 16:
+            # L1's tail queues: the ticket order over each XCD's last units
+            orders = r.buf.tail_orders().cpu().numpy()
+            for x, want in enumerate(tail_orders(counts, m_tile, nb, cuts)):
+                assert np.array_equal(orders[x, :len(want)], want), \
+                    f"L1 tail ticket order differs (XCD {x})"
 
 
 def item_split(cnt, m_tile):
@@ -213,6 +219,36 @@ def xcd_cuts(counts, m_tile, nb, max_items):
         prev = v
     cuts.append(units)
     return np.array(cuts, dtype=np.int64)
+
+
+def unit_tiles(counts, m_tile, nb):
+    """Token tiles of every big-GEMM unit in the kernels' numbering: expert
+    by expert, block-major (unit nb*i0 + bx*n + j is block bx of the
+    expert's item j); item j holds min(cnt, (j+1)*sz) - j*sz rows."""
+    out = []
+    for cnt in np.asarray(counts).tolist():
+        nm, sz = item_split(cnt, m_tile)
+        tiles = [min(-(-(min(cnt, (j + 1) * sz) - j * sz) // 16), 16) for j in range(nm)]
+        out += tiles * nb
+    return np.array(out, dtype=np.int64)
+
+
+def tail_orders(counts, m_tile, nb, cuts):
+    """Per XCD x, the ticket order of L1's tail queue, restated: the last
+    t = min(range, 32) units of [cuts[x], cuts[x+1]) sorted by token tiles,
+    descending, ties in unit order, when some item holds more than 32 rows
+    (else unit order); entry k = the tail index (0..t-1) of the unit that
+    ticket k runs."""
+    tiles = unit_tiles(counts, m_tile, nb)
+    if max((item_split(int(cnt), m_tile)[1] for cnt in counts), default=0) <= 32:
+        tiles = np.zeros_like(tiles)
+    res = []
+    for x in range(8):
+        lo, hi = int(cuts[x]), int(cuts[x + 1])
+        t = min(hi - lo, 32)
+        seg = tiles[hi - t:hi]
+        res.append(np.array(sorted(range(t), key=lambda i: (-seg[i], i)), dtype=np.uint8))
+    return res
 
 
 def _bad(got, want, rel, abs_tol):

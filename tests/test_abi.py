@@ -144,3 +144,36 @@ def test_xcd_ranges_partition_units_and_balance_cost():
         cost = np.repeat(uc, nb * nm)
         per = np.array([cost[a:b].sum() for a, b in zip(cuts[:-1], cuts[1:])])
         assert per.max() - per.min() <= 2 * 18 + 1, per
+
+
+def test_tail_ticket_orders_put_costly_units_first():
+    """The tail queues' ticket order (restated in moe_case.tail_orders): per XCD
+    a permutation of its last min(range, 32) units whose token tiles never
+    rise along the tickets, ties in unit order.  Unit tiles are checked
+    against a direct walk of the item table (block-major units)."""
+    import moe_case as mc
+    rng = np.random.default_rng(11)
+    for E, mean, m_tile, nb in ((8, 20, 64, 16), (256, 64, 256, 16), (256, 260, 256, 24),
+                                (64, 40, 128, 24)):
+        counts = rng.poisson(mean, size=E)
+        counts[rng.integers(0, E, size=3)] *= 9   # hot experts split into several items
+        counts[rng.integers(0, E)] = 0
+        max_items = int(counts.sum() // m_tile + E)
+        tiles = mc.unit_tiles(counts, m_tile, nb)
+        # direct: unit u of expert e's range is item (u - first) % nm's block
+        direct = []
+        for cnt in counts.tolist():
+            nm, sz = mc.item_split(cnt, m_tile)
+            rows = [min(cnt, (j + 1) * sz) - j * sz for j in range(nm)]
+            for lu in range(nb * nm):
+                direct.append(min((rows[lu % nm] + 15) // 16, 16))
+        assert tiles.tolist() == direct
+        cuts = mc.xcd_cuts(counts, m_tile, nb, max_items)
+        for x, order in enumerate(mc.tail_orders(counts, m_tile, nb, cuts)):
+            t = min(int(cuts[x + 1] - cuts[x]), 32)
+            assert sorted(order.tolist()) == list(range(t))
+            seq = tiles[int(cuts[x + 1]) - t + order.astype(np.int64)]
+            assert np.all(np.diff(seq) <= 0), seq
+            for a, b in zip(order[:-1], order[1:]):
+                if seq[list(order).index(a)] == seq[list(order).index(b)]:
+                    assert a < b
