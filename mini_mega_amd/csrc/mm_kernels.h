@@ -50,6 +50,7 @@ constexpr int kQueueL2 = kQueueL1 + kQueueInts;
 constexpr int kQueueTail = 32;      // units per XCD handed out by ticket (one per CU)
 constexpr int kStealers = 8;        // workgroups per XCD past its range that take others' tickets
 static_assert(kQueueTail * 8 <= (kStatusInts - kTailOrdL1) * 4, "the tail order fits");
+constexpr int kTailOrderRows = 128;   // L1's tail order is costliest-first above this item size
 
 // Parameters of the two grouped GEMMs (one struct so that the launcher and
 // the kernels agree on one argument list).

@@ -225,49 +225,52 @@ route_scan_kernel(const int64_t* __restrict__ topk_idx, int P, int chunk,
     // start after light ones at the end of the kernel.  Tail unit i of XCD x
     // is unit cuts[x + 1] - t + i; L1 runs ticket k as tail unit order[k]
     // (gemm_big.hip: claim_tail_unit).  One thread per tail slot finds its
-    // unit's expert by binary search over the item offsets.  When no item
-    // exceeds 32 rows (units of 1-2 tiles, about equal) the order is the
-    // identity and costs nothing.  (Measured on MI355X: a loop over the 8
-    // tails in every expert thread added 10.6 us to this one-workgroup
-    // kernel; L2's tails gained nothing from the order and keep ticket order.)
-    if (e < E) {
-        s_ioff[e] = ioff;
-        s_cnt[e] = cnt;
-    }
-    if (threadIdx.x == 0) s_ioff[E] = nitems;
-    __syncthreads();
-    const bool order_l1 = s_rows > 32;
-    if (threadIdx.x < 8 * kQueueTail) {
-        const int x = threadIdx.x / kQueueTail, i = threadIdx.x % kQueueTail;
-        const int lo = cuts_sh[x], hi = cuts_sh[x + 1], t = min(hi - lo, kQueueTail);
-        if (order_l1 && i < t) {
-            const int u = hi - t + i, im = u / nb1;
-            int a = 0, b = E - 1;   // the last expert whose first item is <= im
-            while (a < b) {
-                const int m = (a + b + 1) >> 1;
-                if (s_ioff[m] <= im) a = m; else b = m - 1;
-            }
-            const int n = max(s_ioff[a + 1] - s_ioff[a], 1), c = s_cnt[a];
-            const int z = (c + n - 1) / n, j = (u - nb1 * s_ioff[a]) % n;
-            tnt[x][i] = (uint8_t)min((min(c, (j + 1) * z) - j * z + 15) >> 4, kBigMaxTiles);
+    // unit's expert by binary search over the item offsets.  Only when some
+    // item holds more than kTailOrderRows rows (skewed routing, T = 8192):
+    // below, the units differ by a few token tiles at most, and the order is
+    // the identity.  (Measured on MI355X: a loop over the 8 tails in every
+    // expert thread added 10.6 us to this one-workgroup kernel; L2's tails
+    // gained nothing from the order and keep ticket order.)
+    uint8_t* order = reinterpret_cast<uint8_t*>(status + kTailOrdL1);
+    __syncthreads();   // cuts_sh, and s_rows of every expert
+    if (s_rows > kTailOrderRows) {   // uniform over the workgroup
+        if (e < E) {
+            s_ioff[e] = ioff;
+            s_cnt[e] = cnt;
         }
-    }
-    __syncthreads();
-    if (threadIdx.x < 8 * kQueueTail) {
-        const int x = threadIdx.x / kQueueTail, i = threadIdx.x % kQueueTail;
-        const int t = min(cuts_sh[x + 1] - cuts_sh[x], kQueueTail);
-        if (i < t) {
-            int r = i;
-            if (order_l1) {
+        if (threadIdx.x == 0) s_ioff[E] = nitems;
+        __syncthreads();
+        if (threadIdx.x < 8 * kQueueTail) {
+            const int x = threadIdx.x / kQueueTail, i = threadIdx.x % kQueueTail;
+            const int lo = cuts_sh[x], hi = cuts_sh[x + 1], t = min(hi - lo, kQueueTail);
+            if (i < t) {
+                const int u = hi - t + i, im = u / nb1;
+                int a = 0, b = E - 1;   // the last expert whose first item is <= im
+                while (a < b) {
+                    const int m = (a + b + 1) >> 1;
+                    if (s_ioff[m] <= im) a = m; else b = m - 1;
+                }
+                const int n = max(s_ioff[a + 1] - s_ioff[a], 1), c = s_cnt[a];
+                const int z = (c + n - 1) / n, j = (u - nb1 * s_ioff[a]) % n;
+                tnt[x][i] = (uint8_t)min((min(c, (j + 1) * z) - j * z + 15) >> 4, kBigMaxTiles);
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < 8 * kQueueTail) {
+            const int x = threadIdx.x / kQueueTail, i = threadIdx.x % kQueueTail;
+            const int t = min(cuts_sh[x + 1] - cuts_sh[x], kQueueTail);
+            if (i < t) {
                 const int v = tnt[x][i];
-                r = 0;
+                int r = 0;
                 for (int k = 0; k < t; ++k) {
                     const int w = tnt[x][k];
                     r += (w > v) || (w == v && k < i);
                 }
+                order[kQueueTail * x + r] = (uint8_t)i;
             }
-            reinterpret_cast<uint8_t*>(status + kTailOrdL1)[kQueueTail * x + r] = (uint8_t)i;
         }
+    } else if (threadIdx.x < 8 * kQueueTail) {
+        order[threadIdx.x] = (uint8_t)(threadIdx.x % kQueueTail);
     }
 }
 

@@ -236,11 +236,11 @@ def unit_tiles(counts, m_tile, nb):
 def tail_orders(counts, m_tile, nb, cuts):
     """Per XCD x, the ticket order of L1's tail queue, restated: the last
     t = min(range, 32) units of [cuts[x], cuts[x+1]) sorted by token tiles,
-    descending, ties in unit order, when some item holds more than 32 rows
+    descending, ties in unit order, when some item holds more than 128 rows
     (else unit order); entry k = the tail index (0..t-1) of the unit that
     ticket k runs."""
     tiles = unit_tiles(counts, m_tile, nb)
-    if max((item_split(int(cnt), m_tile)[1] for cnt in counts), default=0) <= 32:
+    if max((item_split(int(cnt), m_tile)[1] for cnt in counts), default=0) <= 128:
         tiles = np.zeros_like(tiles)
     res = []
     for x in range(8):
