@@ -110,18 +110,10 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(x, xsf, idx, wts, w1, s1, w2, s2, counts, T):
-    """The oracle's check.cu host chain (route -> ref_l1 -> UE8M0 requant ->
-    ref_l2 -> bf16 -> ref_reduce, src/bench_check.cuh:435-499) over the WHOLE
-    layer, timed on this host: with 16 threads (test/check.cu:154-165
-    parallel_rows caps its threads at 16) and with every core the process may
-    use; plus check.cu's own as-is subset (<= 16 rows of the busiest expert,
-    test/check.cu:346)."""
+def _unpack_weights(w1, s1, w2, s2):
+    """Logical row-major fp8 weights and scales on the host (the oracle's input)."""
     import torch
     from mini_mega_amd import inputs
-    from oracle import oracle as orc
-
-    t0 = time.perf_counter()
     a1 = w1.view(torch.uint8).cpu().numpy()
     a2 = w2.view(torch.uint8).cpu().numpy()
     w1l = np.empty((E, 2 * I, H), np.uint8)
@@ -129,47 +121,97 @@ def cpu_baseline(x, xsf, idx, wts, w1, s1, w2, s2, counts, T):
     for e in range(E):
         w1l[e] = inputs.unpack_tiles(a1[e].ravel(), 2 * I, H)
         w2l[e] = inputs.unpack_tiles(a2[e].ravel(), H, I)
-    del a1, a2
-    s1l = np.ascontiguousarray(s1.cpu().numpy())
-    s2l = np.ascontiguousarray(s2.cpu().numpy())
+    return (w1l, np.ascontiguousarray(s1.cpu().numpy()), w2l,
+            np.ascontiguousarray(s2.cpu().numpy()))
+
+
+# Tokens of the bounded CPU sample beyond which a config is timed on a token
+# subset and extrapolated linearly (the host chain's work is linear in the
+# routed pairs once every expert is active).
+CPU_SAMPLE_TOKENS = 2048
+
+
+def cpu_baseline(cpu_inputs, w, head_name):
+    """The oracle's check.cu host chain (route -> ref_l1 -> UE8M0 requant ->
+    ref_l2 -> bf16 -> ref_reduce, src/bench_check.cuh:435-499), timed on this
+    host with 16 threads (test/check.cu:154-165 parallel_rows caps its threads
+    at 16).  The headline config runs the WHOLE layer, also with every core the
+    process may use, plus check.cu's own as-is subset (<= 16 rows of the
+    busiest expert, test/check.cu:346).  Every other config runs the whole
+    layer when it has at most CPU_SAMPLE_TOKENS tokens, else its first
+    CPU_SAMPLE_TOKENS tokens (every expert active), extrapolated linearly in
+    the tokens and labelled so."""
+    from oracle import oracle as orc
+
+    (w1, s1), (w2, s2) = w
+    t0 = time.perf_counter()
+    w1l, s1l, w2l, s2l = _unpack_weights(w1, s1, w2, s2)
     _log(f"cpu baseline: weights unpacked in {time.perf_counter() - t0:.1f} s")
     usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    lb = layer_bytes(counts, T)
-    runs = {}
-    for label, threads in (("16", 16), ("all", int(usable or 1))):
+    G = min(256, I)
+
+    def run(x, xsf, idx, wts, threads):
         t0 = time.perf_counter()
-        orc.layer(x, xsf, w1l, s1l, w2l, s2l, idx, wts, E=E, G=min(256, I), scaled=True,
-                  nthreads=threads)
-        dt = time.perf_counter() - t0
-        runs[label] = (threads, dt)
-        _log(f"cpu baseline: whole layer with {threads} threads {dt:.2f} s")
-    # check.cu's as-is L1/L2 subset: <= 16 rows of the busiest expert
-    ex = int(np.argmax(counts))
-    _, offsets, perm, _ = orc.route(idx, E)
-    rows = min(16, int(counts[ex]))
-    toks = (perm[offsets[ex]:offsets[ex] + rows] // K).astype(np.int64)
-    t0 = time.perf_counter()
-    h = orc.l1_rows(np.ascontiguousarray(x[toks]), np.ascontiguousarray(xsf[toks]), w1l[ex],
-                    np.ascontiguousarray(s1l[ex]), min(256, I))
-    q, qs = orc.quant_ffn(h, True)
-    orc.l2_rows(q, qs, w2l[ex], np.ascontiguousarray(s2l[ex]))
-    subset_s = time.perf_counter() - t0
-    th16, dt16 = runs["16"]
-    thall, dtall = runs["all"]
-    return {
-        "value": round(lb / dt16 / 1e9, 4), "unit": "GB/s", "cores": th16, "kind": "port",
-        "layer_ms": round(dt16 * 1e3, 1),
-        "sample": (f"whole layer T={T} (all {int((counts > 0).sum())} active experts, "
-                   f"{int(counts.sum())} routed pairs): the oracle's C restatement of the "
-                   f"check.cu host chain, {th16} threads (parallel_rows' cap)"),
-        "all_cores": {"threads": thall, "layer_ms": round(dtall * 1e3, 1),
-                      "value": round(lb / dtall / 1e9, 4)},
-        "checkcu_subset": {"rows": rows, "expert": ex, "ms": round(subset_s * 1e3, 1),
-                           "what": "ref_l1 + quantise + ref_l2 on <= 16 rows of the busiest "
-                                   "expert, single thread (test/check.cu:346)"},
-        "host": {"cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
-                 "usable_cores": usable},
-    }
+        orc.layer(x, xsf, w1l, s1l, w2l, s2l, idx, wts, E=E, G=G, scaled=True, nthreads=threads)
+        return time.perf_counter() - t0
+
+    out, per_config = None, {}
+    for name, (x, xsf, idx, wts, counts) in cpu_inputs.items():
+        T = int(x.shape[0])
+        lb = layer_bytes(counts, T)
+        if name == head_name:
+            runs = {}
+            for label, threads in (("16", 16), ("all", int(usable or 1))):
+                runs[label] = (threads, run(x, xsf, idx, wts, threads))
+                _log(f"cpu baseline T={T}: whole layer with {threads} threads "
+                     f"{runs[label][1]:.2f} s")
+            ex = int(np.argmax(counts))
+            _, offsets, perm, _ = orc.route(idx, E)
+            rows = min(16, int(counts[ex]))
+            toks = (perm[offsets[ex]:offsets[ex] + rows] // K).astype(np.int64)
+            t0 = time.perf_counter()
+            h = orc.l1_rows(np.ascontiguousarray(x[toks]), np.ascontiguousarray(xsf[toks]),
+                            w1l[ex], np.ascontiguousarray(s1l[ex]), G)
+            q, qs = orc.quant_ffn(h, True)
+            orc.l2_rows(q, qs, w2l[ex], np.ascontiguousarray(s2l[ex]))
+            subset_s = time.perf_counter() - t0
+            th16, dt16 = runs["16"]
+            thall, dtall = runs["all"]
+            out = {
+                "value": round(lb / dt16 / 1e9, 4), "unit": "GB/s", "cores": th16,
+                "kind": "port", "layer_ms": round(dt16 * 1e3, 1),
+                "sample": (f"whole layer T={T} (all {int((counts > 0).sum())} active experts, "
+                           f"{int(counts.sum())} routed pairs): the oracle's C restatement of "
+                           f"the check.cu host chain, {th16} threads (parallel_rows' cap)"),
+                "all_cores": {"threads": thall, "layer_ms": round(dtall * 1e3, 1),
+                              "value": round(lb / dtall / 1e9, 4),
+                              "note": ("the process may use exactly 16 cores here, so this "
+                                       "run and the 16-thread one coincide")
+                              if thall == th16 else "every core the process may use"},
+                "checkcu_subset": {"rows": rows, "expert": ex, "ms": round(subset_s * 1e3, 1),
+                                   "what": "ref_l1 + quantise + ref_l2 on <= 16 rows of the "
+                                           "busiest expert, single thread (test/check.cu:346)"},
+                "host": {"cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+                         "usable_cores": usable},
+            }
+            continue
+        n = min(T, CPU_SAMPLE_TOKENS)
+        sl = slice(0, n)
+        dt = run(np.ascontiguousarray(x[sl]), np.ascontiguousarray(xsf[sl]),
+                 np.ascontiguousarray(idx[sl]), np.ascontiguousarray(wts[sl]), 16)
+        layer_s = dt * T / n
+        _log(f"cpu baseline T={T}: {n} tokens with 16 threads {dt:.2f} s"
+             + (f" -> whole layer {layer_s:.1f} s (extrapolated)" if n < T else ""))
+        per_config[name] = {
+            "layer_ms": round(layer_s * 1e3, 1), "value": round(lb / layer_s / 1e9, 4),
+            "unit": "GB/s", "cores": 16,
+            "timed": ("whole layer" if n == T else
+                      f"extrapolated x{T / n:g} (linear in tokens) from the first {n} tokens' "
+                      f"chain, timed {dt * 1e3:.0f} ms"),
+        }
+    if out is not None:
+        out["configs"] = per_config
+    return out
 
 
 def measured_peaks(torch, L, stream):
@@ -359,9 +401,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-probes", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
-    ap.add_argument("--tk-info", default=None,
+    ap.add_argument("--tk-info", default=os.path.join("tests", "golden", "tk_real_decode.log"),
                     help="also replay every launch of a TK_INFO routing log (the reference "
-                         "bench's --tk-info), e.g. tests/golden/tk_real_decode.log")
+                         "bench's --tk-info); default: the committed excerpt of the real "
+                         "GLM-5.2 decode corpus")
+    ap.add_argument("--no-tk-info", action="store_true", help="skip the TK_INFO replay")
     ap.add_argument("--tk-max", type=int, default=0, help="at most this many --tk-info launches")
     ap.add_argument("--fuse-l1l2", action="store_true",
                     help="time the layer with L1 and L2 in one launch (MegaLaunchArgs::fuse_l1l2)")
@@ -394,7 +438,7 @@ def main():
     w = inputs.make_weights_normal(E, H, I, seed=args.seed + 1)
     torch.cuda.synchronize()
 
-    results, cpu_inputs = {}, None
+    results, cpu_inputs = {}, {}
     for i, n in enumerate(names):
         T, zipf = CONFIGS[n]
         _log(f"config T={T} zipf={zipf}: {args.warmup} warmup + {args.steps} timed steps")
@@ -402,8 +446,7 @@ def main():
                              args.steps, args.warmup, args.kernel_iters, fuse=args.fuse_l1l2)
         res["workload"] = f"T={T}" + (f" zipf({zipf})" if zipf else " balanced")
         results[n] = res
-        if i == 0:
-            cpu_inputs = ci
+        cpu_inputs[n] = ci
         _log(f"  layer {res['layer_us']} us, {res['tflops']} TFLOP/s, "
              f"HBM {res['hbm_frac']:.3f}, kernels {res['kernels_us']}")
 
@@ -450,18 +493,18 @@ def main():
             "frac_of_fp8_peak": round(r["l1"]["TFLOPs"] / FP8_PEAK_TFLOPS, 4),
             "layer_frac_of_fp8_peak": r["fp8_mfma_frac"],
             "note": "the GEMMs run on the bf16 MFMA (exact fp8 -> bf16 operands)"}
-    if args.tk_info:
-        _log(f"tk_info replay of {args.tk_info}")
-        out["tk_info"] = run_tk_info(torch, mm, inputs, L, stream, w, args.tk_info, 10, 2,
+    if args.tk_info and not args.no_tk_info:
+        path = args.tk_info if os.path.isabs(args.tk_info) else os.path.join(ROOT, args.tk_info)
+        _log(f"tk_info replay of {path}")
+        out["tk_info"] = run_tk_info(torch, mm, inputs, L, stream, w, path, 10, 2,
                                      args.seed + 500, args.tk_max)
+        out["tk_info"]["file"] = os.path.relpath(path, ROOT)
     if not args.no_probes:
         _log("measured peaks")
         out["measured_peaks"] = measured_peaks(torch, L, stream)
-    if not args.no_cpu_baseline and cpu_inputs is not None:
+    if not args.no_cpu_baseline and cpu_inputs:
         _log("cpu baseline")
-        x, xsf, idx, wts, counts = cpu_inputs
-        (w1, s1), (w2, s2) = w
-        out["cpu_baseline"] = cpu_baseline(x, xsf, idx, wts, w1, s1, w2, s2, counts, T0)
+        out["cpu_baseline"] = cpu_baseline(cpu_inputs, w, head_name)
     print(json.dumps(out), flush=True)
 
 

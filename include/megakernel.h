@@ -136,6 +136,10 @@ struct MegaLaunchArgs {
                                            // for 17-128 routed rows per expert on average),
                                            // one workgroup per CU walks the units, streaming
                                            // the next unit's weights during the current one
+    int ready_bias = 0;                    // test hook (fuse_l1l2): added to the count of L1
+                                           // blocks an L2 unit waits for; > 0 makes every
+                                           // wait give up after max_spins polls, so a test
+                                           // drives the bounded wait's timeout report
 };
 
 // Byte offsets of every region inside the workspace (the single-GPU
@@ -262,7 +266,10 @@ int mm_launch_full(const fp8mega::MegaLaunchArgs* a, void* stream);
 // ~550 tokens at E=256, top-8, H=6144, I=2048).  The caller still passes the
 // inputs and outputs.  The call allocates nothing.  Every call on one GPU
 // shares that array: calls that overlap on one GPU (other streams, other
-// threads) race; skip_prologue reuses the previous call's routing.
+// threads) race.  skip_prologue reuses the routing of the previous routed
+// call on this GPU, and is rejected with kErrUnsupported (before any launch)
+// unless that call had the same num_experts, topk, hidden, intermediate,
+// max_tokens, win_cap and tokens.
 int mm_launch_full_noalloc(const fp8mega::MegaLaunchArgs* a, void* stream);
 long long mm_noalloc_scratch_bytes(void);
 int mm_launch_empty(int grid, int threads, long long smem, void* stream);
@@ -295,7 +302,7 @@ int mm_probe_mfma_dot(const uint8_t* a, const uint8_t* b, int K, int N, int mode
                       void* stream);
 // The layer's L2 recomputed over routed slots, out[s][n] fp32 ([P][H]):
 // groups holds ngroups int4 {expert, first slot, end slot, 0} of at most 16
-// slots each; ffn [P][I] + ffn_sf [P][I/128] as L1 writes them, w2 logical
+// slots each (an empty group writes nothing); ffn [P][I] + ffn_sf [P][I/128] as L1 writes them, w2 logical
 // row-major [E][H][I] + w2_sf [E][H/128][I/128].  mode 0: the 16x16x128 fp8
 // MFMA with the UE8M0 bytes as its scale operands; mode 1: the bf16 MFMA
 // after the exact conversion, in the L2 GEMM's operand roles and k order.

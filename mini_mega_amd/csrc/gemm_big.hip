@@ -37,6 +37,12 @@
 // src/compute_big.cuh:1948-1997).
 #include "mm_kernels.h"
 
+// The kernels are written for gfx950 alone (MFMA shapes, buffer-resource
+// words, cache-policy bits and the fused handoff's store semantics).
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "gemm_big.hip is built for gfx950 only"
+#endif
+
 namespace mm {
 
 constexpr int kXTileBytes = 16 * kTileK * 2;   // one bf16 token tile: 16 rows x 128 k
@@ -558,9 +564,10 @@ __device__ __forceinline__ int l1_tile_row(int bx, int bt, int G) {
 
 // kFused: the L2 units of the same launch read this item's ffn rows (the
 // fused L1 -> L2 handoff).  The rows and scales are then written with
-// device-scope relaxed stores (write-through: no L2 write-back release is
-// needed), every wave waits for its stores, and one thread bumps the item's
-// ready counter after the workgroup barrier.
+// agent-scope relaxed atomic stores (on gfx950 write-through stores, so the
+// release below has few dirty L2 lines to write back), every wave waits for
+// its stores, and after the workgroup barrier one thread bumps the item's
+// ready counter with an agent-scope release; the L2 side acquires it.
 template <int W, int NT, bool kFused, class ScalesF>
 __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
                                             ScalesF stage_scales) {
@@ -660,7 +667,7 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
         __builtin_amdgcn_s_waitcnt(0);   // this wave's stores are complete at device scope
         __syncthreads();
         if (threadIdx.x == 0)
-            __hip_atomic_fetch_add(p.ready + it.item, 1, __ATOMIC_RELAXED,
+            __hip_atomic_fetch_add(p.ready + it.item, 1, __ATOMIC_RELEASE,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -775,6 +782,9 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
 // L1 blocks of an item), polling with a sleep; after p.spin_limit polls the
 // workgroup gives up, sets kStatusWaitTimeout in the status word and goes on
 // (the output is then wrong and the status says so; the kernel never hangs).
+// After the poll, an agent-scope acquire fence pairs with the L1 units'
+// release increments, and the workgroup barrier carries it to every wave;
+// the rows are then read with sc1 (device-coherent) loads.
 template <int W, bool kFused>
 __device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_unit, int L,
                                        int grid) {
@@ -799,6 +809,7 @@ __device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_
                     }
                     __builtin_amdgcn_s_sleep(8);
                 }
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             }
             __syncthreads();
         }

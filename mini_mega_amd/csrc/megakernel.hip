@@ -324,7 +324,7 @@ int do_l1_l2_fused(const MegaLaunchArgs& a, hipStream_t s) {
     p2.queue = at<int>(b, b.L.status) + mm::kQueueL2;
     for (mm::GemmParams* q : {&p1, &p2}) {
         q->ready = ready;
-        q->ready_target = nb1;
+        q->ready_target = nb1 + (a.ready_bias > 0 ? a.ready_bias : 0);
         q->spin_limit = a.max_spins > 0 ? a.max_spins : mm::kReadySpinLimit;
         q->err = at<int>(b, b.L.status);
     }
@@ -384,13 +384,27 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 std::mutex g_scratch_mu;
 uint8_t* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on the current device, or null (status in *st).
-uint8_t* scratch_on_device(int* st) {
+// What the routing held in a device's scratch was built for: a skip_prologue
+// call reuses it only with the same shape, since the workspace regions it
+// reads (items, slots, XCD cuts) sit at offsets that move with these.
+struct RouteKey {
+    int valid, E, topk, H, I, max_tokens, win_cap, tokens;
+    bool operator==(const RouteKey& o) const {
+        return valid == o.valid && E == o.E && topk == o.topk && H == o.H && I == o.I &&
+               max_tokens == o.max_tokens && win_cap == o.win_cap && tokens == o.tokens;
+    }
+};
+RouteKey g_scratch_route[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, or null (status in *st);
+// *dev_out: the device.
+uint8_t* scratch_on_device(int* st, int* dev_out) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
         *st = kErrLaunch;
         return nullptr;
     }
+    *dev_out = dev;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[dev] == nullptr) {
         void* ptr = nullptr;
@@ -408,8 +422,10 @@ uint8_t* scratch_on_device(int* st) {
 // is ignored, as is a.workspace_bytes).  The layout of a.max_tokens must fit
 // kScratchBytes (kErrScratch otherwise).  Every region the kernels read is
 // written earlier in the same launch (status, histograms, items, slots, the
-// intermediate rows), so nothing needs clearing between calls; with
-// skip_prologue the routing of the previous call on this device is reused.
+// intermediate rows), so nothing needs clearing between calls.  With
+// skip_prologue the routing of the previous routed call on this device is
+// reused; the call is rejected (kErrUnsupported, before any launch) unless
+// that call had the same E, topk, H, I, max_tokens, win_cap and tokens.
 int do_full_noalloc(const MegaLaunchArgs& a, hipStream_t s) {
     const int st0 = check_dims(a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
     if (st0 != kOk) return st0;
@@ -418,13 +434,28 @@ int do_full_noalloc(const MegaLaunchArgs& a, hipStream_t s) {
     const MegaLayout L =
         layout(a.max_tokens, a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
     if (L.total > kScratchBytes) return kErrScratch;
-    int st = kOk;
-    uint8_t* ws = scratch_on_device(&st);
+    int st = kOk, dev = 0;
+    uint8_t* ws = scratch_on_device(&st, &dev);
     if (st != kOk) return st;
+    const RouteKey key{1, a.num_experts, a.topk, a.hidden, a.intermediate, a.max_tokens,
+                       a.win_cap, a.tokens};
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (a.skip_prologue) {
+            if (!(g_scratch_route[dev] == key)) return kErrUnsupported;
+        } else {
+            g_scratch_route[dev] = RouteKey{};   // no usable routing until this call launched
+        }
+    }
     MegaLaunchArgs b = a;
     b.rwk = reinterpret_cast<rwk_data*>(ws);
     b.workspace_bytes = kScratchBytes;
-    return do_full(b, s);
+    st = do_full(b, s);
+    if (st == kOk && !a.skip_prologue) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        g_scratch_route[dev] = key;
+    }
+    return st;
 }
 
 int record(int st) {
@@ -594,7 +625,7 @@ using fp8mega::MegaLaunchArgs;
 
 extern "C" {
 
-int mm_abi_version(void) { return 3; }
+int mm_abi_version(void) { return 4; }
 
 long long mm_noalloc_scratch_bytes(void) { return (long long)fp8mega::kScratchBytes; }
 
@@ -611,7 +642,7 @@ long long mm_args_offset(const char* f) {
     MM_FIELD(hidden) MM_FIELD(intermediate) MM_FIELD(max_tokens) MM_FIELD(workspace_bytes)
     MM_FIELD(x_sf) MM_FIELD(w1_sf) MM_FIELD(w2_sf) MM_FIELD(ffn_ue8m0) MM_FIELD(y_bf16)
     MM_FIELD(fuse_l1l2)
-    MM_FIELD(l2_no_walk)
+    MM_FIELD(l2_no_walk) MM_FIELD(ready_bias)
 #undef MM_FIELD
     return -1;
 }

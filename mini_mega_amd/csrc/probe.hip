@@ -51,7 +51,8 @@ mfma_dot_probe_kernel(const uint8_t* __restrict__ a, const uint8_t* __restrict__
 // end-to-end effect of the MFMA choice: out[s][n] (fp32) = sum_k
 // dec(ffn[s][k]) 2^(ffn_sf[s][k/128] - 127) * dec(w2[e][n][k]) 2^(w2_sf[e][n/128][k/128] - 127)
 // for the slots s in [g.y, g.z) of expert g.x, g = groups[blockIdx.y] (at
-// most 16 slots), and the 16 channels n0 = 16 * blockIdx.x ..  w2 is logical
+// most 16 slots; an empty group, g.z <= g.y, computes and writes nothing),
+// and the 16 channels n0 = 16 * blockIdx.x ..  w2 is logical
 // row-major [E][H][I].  Operand roles and k order are the L2 GEMM's: weights
 // are the A operand, ffn rows the B operand, k ascending.  mode 0:
 // v_mfma_scale_f32_16x16x128_f8f6f4 with the UE8M0 bytes as its scale
@@ -63,6 +64,7 @@ l2_probe_kernel(const uint8_t* __restrict__ ffn, const uint8_t* __restrict__ ffn
                 const int4* __restrict__ groups, int H, int I, int mode, float* __restrict__ out) {
     const int l = threadIdx.x, n0 = blockIdx.x * 16;
     const int4 g = groups[blockIdx.y];
+    if (g.z <= g.y) return;   // empty group: no row to clamp to
     const int KB = I >> 7;
     const int s = min(g.y + (l & 15), g.z - 1);   // rows past the group's end: loaded, not stored
     const int n = n0 + (l & 15);

@@ -39,7 +39,10 @@ ORC_API void orc_set_acc64(int on) { g_acc64 = on; }
  * (0 = none, the only value outside those tests): 1 = the up rows of L1 take
  * their gate rows' 128-row scale block; 2 = the W2 scale block index is
  * transposed ((k/128, n/128) instead of (n/128, k/128)); 3 = the ffn rows
- * take the scale of the next 128-column block. */
+ * take the scale of the next 128-column block; 4 = the 128x128 block cast
+ * multiplies by its scale instead of dividing; 5 = the check.cu x bytes use
+ * the global token in place of the rank-local one; 6 = the check.cu weights
+ * lose their 0.25 * rank term. */
 static int g_mutation = 0;
 ORC_API void orc_set_mutation(int m) { g_mutation = m; }
 
@@ -169,7 +172,8 @@ ORC_API void orc_quant_blocks_ue8m0(const float* w, int rows, int cols, int gran
                 for (int c = 0; c < gran; ++c)
                     amax = fmaxf(amax, fabsf(w[(size_t)(br * gran + r) * cols + bc * gran + c]));
             const uint8_t e = orc_block_scale(amax);
-            const float inv = ldexpf(1.0f, 127 - (int)e);
+            /* mutation 4 (tests only): multiply by the scale instead of its inverse */
+            const float inv = ldexpf(1.0f, g_mutation == 4 ? (int)e - 127 : 127 - (int)e);
             sf[(size_t)br * nbc + bc] = e;
             for (int r = 0; r < gran; ++r)
                 for (int c = 0; c < gran; ++c) {
@@ -194,11 +198,15 @@ ORC_API void orc_checkcu_inputs(int ranks, int tpr, int H, int topk, uint8_t* x,
     for (int r = 0; r < ranks; ++r)
         for (int t = 0; t < tpr; ++t) {
             const size_t g = (size_t)r * tpr + t;
+            /* mutations 5 / 6 (tests only): the global token in place of the
+             * rank-local one in x; the rank term dropped from the weights */
+            const int tx = g_mutation == 5 ? (int)g : t;
             for (int c = 0; c < H; ++c)
-                x[g * H + c] = (uint8_t)((r * 37 + t * 7 + c * 3) & 0x3f);
+                x[g * H + c] = (uint8_t)((r * 37 + tx * 7 + c * 3) & 0x3f);
             for (int k = 0; k < topk; ++k) {
                 const int i = t * topk + k;
-                w[g * topk + k] = 1.0f + (float)r * 0.25f + (float)(i % 7) * 0.01f;
+                const float rt = g_mutation == 6 ? 0.0f : (float)r * 0.25f;
+                w[g * topk + k] = 1.0f + rt + (float)(i % 7) * 0.01f;
             }
         }
 }

@@ -307,10 +307,11 @@ def _dequant_blocks(q, sf):
     return v
 
 
-def check_l1(c: Case, r: Run, e: int, max_rows: int = 64):
+def check_l1(c: Case, r: Run, e: int, max_rows: int | None = 64):
     """Device ffn of expert e vs oracle ref_l1 on the same pool rows."""
     lo, hi, toks = slot_rows(c, r, e)
-    hi = min(hi, lo + max_rows)
+    if max_rows is not None:
+        hi = min(hi, lo + max_rows)
     toks = toks[:hi - lo]
     if hi == lo:
         return
@@ -359,10 +360,11 @@ def check_l1(c: Case, r: Run, e: int, max_rows: int = 64):
     assert flips <= FLIP_MAX, f"L1 expert {e}: {flips:.2%} of bytes differ from the oracle's"
 
 
-def check_l2(c: Case, r: Run, e: int, max_rows: int = 64):
+def check_l2(c: Case, r: Run, e: int, max_rows: int | None = 64):
     """Device L2 rows of expert e vs oracle ref_l2 fed with the device ffn."""
     lo, hi, _ = slot_rows(c, r, e)
-    hi = min(hi, lo + max_rows)
+    if max_rows is not None:
+        hi = min(hi, lo + max_rows)
     if hi == lo:
         return
     ffn = np.ascontiguousarray(r.buf.ffn(hi).cpu().numpy()[lo:hi])

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_args_mirror_matches_c_struct():
     L = mm.lib()
-    assert L.mm_abi_version() == 3
+    assert L.mm_abi_version() == 4
     assert L.mm_args_size() == ctypes.sizeof(mm.MegaLaunchArgs)
     for name, *_ in mm.MegaLaunchArgs._fields_:
         assert L.mm_args_offset(name.encode()) == getattr(mm.MegaLaunchArgs, name).offset

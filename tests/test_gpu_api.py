@@ -350,11 +350,15 @@ def test_l2_walk_matches_one_unit_kernel(E, K, H, I, T, zipf, win, scaled, walks
 
 
 def test_fused_l1l2_bounded_wait_reports_timeout():
-    """With max_spins = 1 an L2 unit polls its item's ready counter once: the
-    launch still ends (every wait is bounded), and a unit that gave up sets
-    kStatusWaitTimeout, which read_status reports as a device error.  The
-    next launch with the default bound is exact again."""
-    _say("fused L1->L2 with max_spins=1")
+    """The fused launch's give-up path, forced from the host: ready_bias = 1
+    raises every L2 unit's ready target past the count its item's L1 blocks
+    reach, and max_spins = 1 bounds each wait to one poll.  Every kernel still
+    ends (every wait is bounded), every L2 unit gives up and sets
+    kStatusWaitTimeout, and read_status reports it as a device error (7).  A
+    launch whose counters all arrive (max_spins = 1, no bias) may or may not
+    time out, and is exact when it does not.  The next launch with the
+    default bound is exact again."""
+    _say("fused L1->L2 give-up: ready_bias=1, max_spins=1")
     E, K, H, I, T = 256, 8, 6144, 2048, 2048
     c = mc.normal_case(E, K, H, I, T, seed=99, scaled=True)
     buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I)
@@ -364,15 +368,25 @@ def test_fused_l1l2_bounded_wait_reports_timeout():
     torch.cuda.synchronize()
     want = y.view(torch.int16).cpu().numpy()
     buf.fuse_l1l2 = True
+    out = (ctypes.c_int * 5)()
+    # forced: every wait gives up
+    a = buf.make_args(T, (c.w1, c.s1), (c.w2, c.s2), y_bf16=y)
+    a.max_spins, a.ready_bias = 1, 1
+    assert mm.lib().mm_launch_full(ctypes.byref(a), _stream()) == 0
+    torch.cuda.synchronize()
+    st = buf.device_status()
+    rc = mm.lib().mm_read_status(ctypes.byref(a), out, 5, _stream())
+    _say(f"  forced: error bits {st['error']}, read_status {rc}")
+    assert st["error"] == 2 and rc == 7
+    # counters that all arrive, one poll each: exact unless a wait gave up
     a = buf.make_args(T, (c.w1, c.s1), (c.w2, c.s2), y_bf16=y)
     a.max_spins = 1
     assert mm.lib().mm_launch_full(ctypes.byref(a), _stream()) == 0
     torch.cuda.synchronize()
     st = buf.device_status()
-    out = (ctypes.c_int * 5)()
     rc = mm.lib().mm_read_status(ctypes.byref(a), out, 5, _stream())
     timed_out = bool(st["error"] & 2)
-    _say(f"  timeout bit set: {timed_out}")
+    _say(f"  unforced: timeout bit set: {timed_out}")
     assert st["error"] & ~2 == 0
     assert rc == (7 if timed_out else 0)
     if not timed_out:

@@ -87,6 +87,42 @@ def test_quant_rows_ue8m0_invariants(scale):
                                     s[:, :, None] * 2.0 ** -10) + 1e-30)
 
 
+def _torch_per_block_cast_ue8m0(w: np.ndarray, gran: int = 128):
+    """utils/math.py:13-16,62-72 (ceil_to_ue8m0, per_block_cast_to_fp8 with
+    use_ue8m0=True) in torch float32 on the CPU, for shapes that are multiples
+    of gran (no padding): fp8 bytes and UE8M0 exponent bytes [rows/g][cols/g]."""
+    x = torch.from_numpy(np.ascontiguousarray(w, np.float32))
+    m, n = x.shape
+    xv = x.view(m // gran, gran, n // gran, gran)
+    amax = xv.abs().float().amax(dim=(1, 3), keepdim=True).clamp(1e-4)
+    sf = amax / 448.0
+    bits = sf.abs().float().view(torch.int32)
+    exp = ((bits >> 23) & 0xFF) + (bits & 0x7FFFFF).bool().int()
+    sf = (exp.clamp(1, 254) << 23).view(torch.float32)
+    q = (xv * (1.0 / sf)).to(torch.float8_e4m3fn).view(m, n)
+    return q.view(torch.uint8).numpy(), ((sf.view(torch.int32) >> 23) & 0xFF).to(
+        torch.uint8).view(m // gran, n // gran).numpy()
+
+
+@pytest.mark.parametrize("scale", [1e-3, 0.02, 5.0])
+def test_quant_blocks_ue8m0_equals_torch_recipe(scale, mutation):
+    """The block cast's bytes and scales against a torch restatement of
+    per_block_cast_to_fp8 (utils/math.py:62-72), bit for bit, with a hot block,
+    an all-zero block (amax clamps to 1e-4) and a tiny one; a planted mistake
+    (the scale multiplied instead of divided) must fail it."""
+    w = (rng.standard_normal((384, 256)) * scale).astype(np.float32)
+    w[:128, :128] *= 64.0
+    w[128:256, 128:] = 0.0
+    w[256:, :128] *= 1e-6
+    tq, tsf = _torch_per_block_cast_ue8m0(w)
+    q, sf = orc.quant_blocks_ue8m0(w)
+    assert np.array_equal(sf, tsf)
+    assert np.array_equal(q, tq)
+    mutation(4)
+    bq, bsf = orc.quant_blocks_ue8m0(w)
+    assert np.array_equal(bsf, tsf) and not np.array_equal(bq, tq)
+
+
 def test_quant_blocks_ue8m0_scale_per_block():
     w = (rng.standard_normal((256, 384)) * 0.02).astype(np.float32)
     w[:128, :128] *= 100.0  # one hot block: its scale must differ from its neighbours'
@@ -271,6 +307,34 @@ def test_reduce_order_and_invalid_pairs():
 
 
 # ------------------------------------------------------- check.cu closed form --
+@pytest.mark.parametrize("ranks,tpr,H,K", [(4, 3, 384, 8), (32, 2, 256, 8), (3, 5, 128, 4)])
+def test_checkcu_inputs_equal_fill_inputs(ranks, tpr, H, K, mutation):
+    """The check.cu inputs against a numpy evaluation of fill_inputs
+    (test/mega_common.cuh:166-175) for every rank: x bytes (r*37 + t*7 +
+    c*3) & 0x3f with t rank-local, weights 1 + 0.25 r + 0.01 (i % 7) with
+    i = t*topk + k, in float32 left to right as the C++ does.  Planted
+    mistakes (the global token in x, the rank term dropped) must fail it."""
+    r = np.arange(ranks)[:, None, None]
+    t = np.arange(tpr)[None, :, None]
+    c = np.arange(H)[None, None, :]
+    want_x = ((r * 37 + t * 7 + c * 3) & 0x3F).astype(np.uint8).reshape(ranks * tpr, H)
+    i = (np.arange(tpr)[:, None] * K + np.arange(K)[None, :])
+    want_w = np.empty((ranks, tpr, K), np.float32)
+    for rr in range(ranks):
+        want_w[rr] = (np.float32(1.0) + np.float32(rr) * np.float32(0.25)) + \
+            (i % 7).astype(np.float32) * np.float32(0.01)
+    want_w = want_w.reshape(ranks * tpr, K)
+    x, w = orc.checkcu_inputs(ranks, tpr, H, K)
+    assert np.array_equal(x, want_x)
+    assert np.array_equal(w.view(np.uint32), want_w.view(np.uint32))
+    mutation(5)
+    bx, _ = orc.checkcu_inputs(ranks, tpr, H, K)
+    assert not np.array_equal(bx, want_x)
+    mutation(6)
+    _, bw = orc.checkcu_inputs(ranks, tpr, H, K)
+    assert not np.array_equal(bw, want_w)
+
+
 def test_checkcu_inputs_saturate_every_ffn_byte():
     """check.cu inputs are all-positive with g, u ~ 4e5..9e5, so every L1
     output saturates to 448 = 0x7E; and g == u because 131*256 = 0 mod 64."""
