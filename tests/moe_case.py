@@ -391,6 +391,43 @@ def check_reduce(c: Case, r: Run):
                                                    .view(np.float32))), "bf16 y differs"
 
 
+def bf16_half_ulp(v: np.ndarray) -> np.ndarray:
+    """Half a bf16 ulp at |v| (8 significant bits): the largest error of a
+    correctly rounded bf16 value of v (normal range)."""
+    a = np.maximum(np.abs(v.astype(np.float64)), 2.0 ** -126)
+    return np.ldexp(1.0, np.floor(np.log2(a)).astype(np.int32) - 8)
+
+
+def e2e_gate(y_bf16: np.ndarray, y32: np.ndarray, y_ref: np.ndarray, what: str = "end-to-end"):
+    """The end-to-end bar (max|d| <= 2e-2 rms(y), cos >= 0.9995) against the
+    oracle's fp32 y, on the device's fp32 y (the reference's MegaLaunchArgs::y
+    output), plus: the bf16 output is the round-to-nearest-even cast of that
+    fp32 y, bit for bit; and the bf16 output's distance to the oracle beyond
+    its own half-ulp rounding stays within the same bar.  The bf16 cast alone
+    can exceed 2e-2 rms(y): at |y| in [4, 8) its half-ulp is 2^-6, i.e.
+    0.029 rms(y) when rms(y) = 0.54 (T=8192 reaches such outputs), so the
+    bar is checked on fp32 and on the bf16 error in excess of that half-ulp.
+    Returns the metrics (and the message) for the caller's report."""
+    err32, rms, cos32 = e2e_metrics(y32, y_ref)
+    errbf, _, cosbf = e2e_metrics(y_bf16, y_ref)
+    d = np.abs(y_bf16.astype(np.float64) - y_ref.astype(np.float64))
+    hu = bf16_half_ulp(np.maximum(np.abs(y32), np.abs(y_ref)))
+    excess = float(np.max(d - hu))
+    cast = torch.from_numpy(np.ascontiguousarray(y32, np.float32)).to(torch.bfloat16).float().numpy()
+    cast_ok = bool(np.array_equal(cast.view(np.uint32), y_bf16.astype(np.float32).view(np.uint32)))
+    ref_bf = torch.from_numpy(np.ascontiguousarray(y_ref, np.float32)).to(torch.bfloat16).float().numpy()
+    bf_diff = float(np.mean(ref_bf != y_bf16))
+    msg = (f"{what}: fp32 max|d|/rms={err32 / rms:.4f} cos={cos32:.7f} (bars "
+           f"{E2E_ABS_FRAC}, {E2E_COS}); bf16 max|d|/rms={errbf / rms:.4f}, beyond half-ulp "
+           f"{excess / rms:.4f}; bf16 == RNE(fp32 y): {cast_ok}; bf16 != bf16(oracle) "
+           f"{bf_diff:.2e}; max|y_ref|/rms={float(np.abs(y_ref).max()) / rms:.2f}")
+    print(f"[e2e] {msg}", flush=True)
+    assert err32 <= E2E_ABS_FRAC * rms and cos32 >= E2E_COS, msg
+    assert cast_ok, msg
+    assert excess <= E2E_ABS_FRAC * rms and cosbf >= E2E_COS, msg
+    return dict(err32=err32, errbf=errbf, rms=rms, cos=cos32, excess=excess, msg=msg)
+
+
 def e2e_metrics(got: np.ndarray, want: np.ndarray):
     got = got.astype(np.float64)
     want = want.astype(np.float64)
@@ -400,23 +437,18 @@ def e2e_metrics(got: np.ndarray, want: np.ndarray):
     return err, rms, cos
 
 
-def check_e2e(c: Case, r: Run, nthreads: int = 16, fp32_output: bool = False):
-    """Whole chain vs the oracle's own chain (no device intermediates).
-    fp32_output compares the device's fp32 sum instead of its bf16 cast (the
-    cast itself is checked bit for bit by check_reduce): with heavy slot-cap
-    drops the outputs are heavy-tailed, and the bf16 half-ulp of one output
-    at ~10x rms(y) alone exceeds 2e-2 rms(y) whatever the GEMMs did."""
+def check_e2e(c: Case, r: Run, nthreads: int = 16):
+    """Whole chain vs the oracle's own chain (no device intermediates), at
+    the end-to-end bar of e2e_gate (fp32 y; bf16 y as its exact cast and
+    beyond its own half-ulp)."""
     w1 = np.stack([c.w1_logical(e) for e in range(c.E)])
     w2 = np.stack([c.w2_logical(e) for e in range(c.E)])
     s1 = None if c.s1 is None else np.ascontiguousarray(c.s1.cpu().numpy())
     s2 = None if c.s2 is None else np.ascontiguousarray(c.s2.cpu().numpy())
     ref = orc.layer(c.x, c.xsf, w1, s1, w2, s2, c.idx, c.wts, E=c.E, G=c.G, scaled=c.scaled,
                     nthreads=nthreads, cap=c.cap if c.cap else None)
-    err, rms, cos = e2e_metrics(r.y32 if fp32_output else r.y, ref["y"])
-    print(f"[e2e] max_abs/rms={err / rms:.4f} cos={cos:.7f}", flush=True)
-    assert err <= E2E_ABS_FRAC * rms and cos >= E2E_COS, (
-        f"end-to-end: max_abs {err:.3e} rms {rms:.3e} cos {cos:.6f}")
-    return err, rms, cos
+    g = e2e_gate(r.y, r.y32, ref["y"])
+    return g["err32"], g["rms"], g["cos"]
 
 
 def check_e2e_tokens(c: Case, r: Run, tokens, nthreads: int = 16):
@@ -435,11 +467,8 @@ def check_e2e_tokens(c: Case, r: Run, tokens, nthreads: int = 16):
     xsf = None if c.xsf is None else np.ascontiguousarray(c.xsf[tokens])
     ref = orc.layer(xs, xsf, w1, s1, w2, s2, idx2, np.ascontiguousarray(c.wts[tokens]),
                     E=len(experts), G=c.G, scaled=c.scaled, nthreads=nthreads)
-    err, rms, cos = e2e_metrics(r.y[tokens], ref["y"])
-    print(f"[e2e tokens] max_abs/rms={err / rms:.4f} cos={cos:.7f}", flush=True)
-    assert err <= E2E_ABS_FRAC * rms and cos >= E2E_COS, (
-        f"end-to-end (token subset): max_abs {err:.3e} rms {rms:.3e} cos {cos:.6f}")
-    return err, rms, cos
+    g = e2e_gate(r.y[tokens], r.y32[tokens], ref["y"], what="end-to-end (token subset)")
+    return g["err32"], g["rms"], g["cos"]
 
 def ref_lane_pack(w):
     """Logical [E][N][K] uint8 -> the reference's on-device lane-tile bytes:

@@ -78,11 +78,10 @@ def test_full_output_end_to_end(T, zipf, chunk):
     ffn_flips = n_ffn / float(ffn_d.size)
     sf_flips = n_sf / float(sf_d.size)
     l2_flips = n_l2 / float(l2_d.size)
-    err, rms, cos = mc.e2e_metrics(r.y, y_ref)
     del w1, w2
-    msg = (f"T={T} zipf={zipf}: max|d|/rms={err / rms:.4f} (bar {mc.E2E_ABS_FRAC}) "
-           f"cos={cos:.7f} (bar {mc.E2E_COS}) ffn byte flips={ffn_flips:.2e} "
-           f"(bar {mc.FLIP_MAX:.0e}) ffn scale diffs={sf_flips:.2e} l2 bf16 diffs={l2_flips:.2e}")
+    msg = (f"T={T} zipf={zipf}: ffn byte flips={ffn_flips:.2e} (bar {mc.FLIP_MAX:.0e}) "
+           f"ffn scale diffs={sf_flips:.2e} l2 bf16 diffs={l2_flips:.2e}")
     _say(f"  {msg} ({time.time() - t0:.0f} s)")
     assert ffn_flips <= mc.FLIP_MAX, msg
-    assert err <= mc.E2E_ABS_FRAC * rms and cos >= mc.E2E_COS, msg
+    g = mc.e2e_gate(r.y, r.y32, y_ref, what=f"T={T} zipf={zipf} full output")
+    _say(f"  {g['msg']}")

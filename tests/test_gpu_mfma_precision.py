@@ -13,9 +13,9 @@ products of fp8 e4m3 operands (the values the layer multiplies).
 The bf16 MFMA sums to ~1e-8 of sum|terms| and flips almost nothing; the fp8
 MFMA truncates to ~2^-20 of sum|terms| and flips orders of magnitude more.
 The last test carries that to the whole layer for L2 alone (the GEMM whose
-only exposure is its bf16 output rounding): on Zipf(1.1) T=2048 it measured
-max|d| = 0.0332 rms(y) against the bar of 0.02 (0.0189 with the bf16 MFMA),
-the reason both GEMMs run on the bf16 MFMA."""
+only exposure is its bf16 output rounding) on Zipf(1.1) T=2048, and measures
+what a bounded-error fp8 L2 with a recompute of the outputs near a bf16
+rounding midpoint would have to recompute."""
 import sys
 
 import numpy as np
@@ -156,15 +156,57 @@ def test_l2_mfma_choice_end_to_end():
                                        out.data_ptr(), torch.cuda.current_stream().cuda_stream)
         assert rc == 0
         torch.cuda.synchronize()
-        bits = orc.f32_to_bf16(out.cpu().numpy().ravel()).reshape(slots, H)
-        _, yb = orc.reduce(np.ascontiguousarray(bits), r.pair_pos.reshape(T, K), c.wts, T, K)
-        y = (yb.astype(np.uint32) << 16).view(np.float32).reshape(T, H)
-        err, rms, cos = mc.e2e_metrics(y, ref["y"])
+        o32 = out.cpu().numpy()
+        bits = orc.f32_to_bf16(o32.ravel()).reshape(slots, H)
+        y32, yb = orc.reduce(np.ascontiguousarray(bits), r.pair_pos.reshape(T, K), c.wts, T, K)
+        yb = (yb.astype(np.uint32) << 16).view(np.float32).reshape(T, H)
+        err32, rms, cos = mc.e2e_metrics(y32, ref["y"])
+        errbf, _, _ = mc.e2e_metrics(yb, ref["y"])
+        excess = float(np.max(np.abs(yb.astype(np.float64) - ref["y"])
+                              - mc.bf16_half_ulp(np.maximum(np.abs(y32), np.abs(ref["y"])))))
         l2_diff = float(np.mean(bits != ref["l2"]))
-        res[name] = (err / rms, cos, bits)
-        _say(f"L2 on the {name} MFMA, Zipf(1.1) T=2048: max|d|/rms={err / rms:.4f} "
-             f"cos={cos:.7f}; L2 bf16 outputs differing from the oracle {l2_diff:.3%}")
+        res[name] = (err32 / rms, cos, bits, o32, excess / rms)
+        _say(f"L2 on the {name} MFMA, Zipf(1.1) T=2048: fp32 y max|d|/rms={err32 / rms:.4f} "
+             f"cos={cos:.7f}; bf16 y max|d|/rms={errbf / rms:.4f}, beyond its half-ulp "
+             f"{excess / rms:.4f}; L2 bf16 outputs differing from the oracle {l2_diff:.3%}")
     assert np.array_equal(res["bf16"][2], dev_l2), "bf16 recomputation differs from the layer's L2"
     assert res["bf16"][0] <= mc.E2E_ABS_FRAC and res["bf16"][1] >= mc.E2E_COS
-    # L2 on the fp8 MFMA breaks the end-to-end bar on this config
-    assert res["fp8"][0] > mc.E2E_ABS_FRAC > res["bf16"][0]
+    assert res["bf16"][4] <= mc.E2E_ABS_FRAC
+    # the fp8 MFMA's coarser sums move y further from the oracle than the bf16 MFMA's
+    assert res["fp8"][0] > res["bf16"][0]
+
+    # A bounded-error fp8 L2: its fp32 sum is within eps * sum|terms| of the
+    # exact one (eps: twice the largest error the L2-shape probe measured,
+    # 2^-18.8), so its bf16 rounding is certain wherever the sum lies farther
+    # than that from a bf16 rounding midpoint; a fix-up pass would recompute
+    # only the other outputs.  Measured here: the share it must recompute,
+    # and that the outputs it keeps round exactly as the bf16 MFMA's.
+    eps = 2.0 ** -17.8
+    table = torch.from_numpy(orc.e4m3_decode_table().astype(np.float32)).cuda()
+    a_abs = table[ffn.long()].abs() * torch.pow(
+        2.0, ffn_sf.float() - 127.0).repeat_interleave(128, dim=1)
+    terms = torch.empty((slots, H), dtype=torch.float32, device="cuda")
+    for e in range(E):
+        lo, hi = int(r.offsets[e]), int(r.offsets[e + 1])
+        if hi == lo:
+            continue
+        sc = torch.pow(2.0, c.s2[e].float() - 127.0)
+        b_abs = table[dw2[e].long()].abs() * sc.repeat_interleave(128, 0).repeat_interleave(128, 1)
+        terms[lo:hi] = a_abs[lo:hi] @ b_abs.T
+    terms = terms.cpu().numpy().astype(np.float64) * 1.01   # fp32 GEMM of |terms|: margin
+    o8 = res["fp8"][3]
+    u = o8.view(np.uint32)
+    mag = np.maximum(np.abs(o8.astype(np.float64)), 2.0 ** -126)
+    ulp32 = np.ldexp(1.0, np.floor(np.log2(mag)).astype(np.int32) - 23)
+    to_mid = np.abs((u & 0xFFFF).astype(np.float64) - 32768.0) * ulp32
+    flag = to_mid <= eps * terms
+    share = float(np.mean(flag))
+    kept = ~flag
+    kept_diff = float(np.mean(res["fp8"][2][kept] != res["bf16"][2][kept]))
+    fixed = np.where(flag, res["bf16"][2], res["fp8"][2])
+    _say(f"bounded-error fp8 L2 (eps = 2^-17.8 sum|terms|): {share:.3%} of outputs flagged for "
+         f"recompute; kept outputs differing from the bf16 MFMA's {kept_diff:.2e}; after the "
+         f"fix-up {float(np.mean(fixed != res['bf16'][2])):.2e}")
+    # the kept outputs round as the bf16 MFMA's (which sums to ~2^-25.6 sum|terms|)
+    assert kept_diff <= 1e-6
+    assert 0.0 < share < 1.0

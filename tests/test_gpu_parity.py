@@ -2,7 +2,8 @@
 
 Bars: routing / permutation / counts / byte work bit-exact; L1, L2, REDUCE at
 check.cu's staged tolerances; the whole layer at max|d| <= 2e-2 rms(y) and
-cos >= 0.9995.
+cos >= 0.9995 on the fp32 y, with the bf16 y its exact RNE cast and within
+the same bar beyond its own half-ulp (moe_case.e2e_gate).
 """
 import ctypes
 import dataclasses
@@ -541,8 +542,7 @@ def _sweep_case(seed):
 def test_random_shapes_sweep(seed):
     """Random small layers (seeded): routing bit-exact, L1 / L2 on the busiest
     and one other active expert at the staged tolerances, REDUCE, and the
-    whole layer at the end-to-end bar (on the fp32 output where a slot cap
-    drops pairs: see moe_case.check_e2e); then the same layer with L1 and L2
+    whole layer at the end-to-end bar (moe_case.e2e_gate); then the same layer with L1 and L2
     in one launch (fuse_l1l2) on the same buffer, bit-identical."""
     c, zipf = _sweep_case(seed)
     _say(f"sweep seed={seed}: E={c.E} K={c.K} H={c.H} I={c.I} T={c.T} scaled={c.scaled} "
@@ -557,7 +557,7 @@ def test_random_shapes_sweep(seed):
             mc.check_l1(c, r, e)
             mc.check_l2(c, r, e)
     mc.check_reduce(c, r)
-    err, rms, cos = mc.check_e2e(c, r, fp32_output=bool(c.cap))
+    err, rms, cos = mc.check_e2e(c, r)
     _say(f"  e2e max_abs={err:.3e} rms={rms:.3e} cos={cos:.6f}")
     r.buf.fuse_l1l2 = True
     r2 = mc.run_layer(c, buf=r.buf)
