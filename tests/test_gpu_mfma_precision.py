@@ -175,12 +175,14 @@ def test_l2_mfma_choice_end_to_end():
     # the fp8 MFMA's coarser sums move y further from the oracle than the bf16 MFMA's
     assert res["fp8"][0] > res["bf16"][0]
 
-    # A bounded-error fp8 L2: its fp32 sum is within eps * sum|terms| of the
-    # exact one (eps: twice the largest error the L2-shape probe measured,
-    # 2^-18.8), so its bf16 rounding is certain wherever the sum lies farther
-    # than that from a bf16 rounding midpoint; a fix-up pass would recompute
-    # only the other outputs.  Measured here: the share it must recompute,
-    # and that the outputs it keeps round exactly as the bf16 MFMA's.
+    # A bounded-error fp8 L2: where its fp32 sum lies farther than eps *
+    # sum|terms| from a bf16 rounding midpoint, its bf16 rounding would be
+    # certain if eps bounded its error, and a fix-up pass would recompute only
+    # the other outputs.  eps: twice the largest error the L2-shape probe
+    # measured (2^-18.8).  Measured here: the share such a pass must
+    # recompute, and how many of the outputs it would keep still round away
+    # from the bf16 MFMA's (a share > 0 means eps does not bound the error on
+    # the layer's own data).
     eps = 2.0 ** -17.8
     table = torch.from_numpy(orc.e4m3_decode_table().astype(np.float32)).cuda()
     a_abs = table[ffn.long()].abs() * torch.pow(
@@ -203,10 +205,10 @@ def test_l2_mfma_choice_end_to_end():
     share = float(np.mean(flag))
     kept = ~flag
     kept_diff = float(np.mean(res["fp8"][2][kept] != res["bf16"][2][kept]))
-    fixed = np.where(flag, res["bf16"][2], res["fp8"][2])
     _say(f"bounded-error fp8 L2 (eps = 2^-17.8 sum|terms|): {share:.3%} of outputs flagged for "
-         f"recompute; kept outputs differing from the bf16 MFMA's {kept_diff:.2e}; after the "
-         f"fix-up {float(np.mean(fixed != res['bf16'][2])):.2e}")
-    # the kept outputs round as the bf16 MFMA's (which sums to ~2^-25.6 sum|terms|)
-    assert kept_diff <= 1e-6
-    assert 0.0 < share < 1.0
+         f"recompute; kept outputs rounding away from the bf16 MFMA's {kept_diff:.2e}")
+    # Cost model: a flagged output is a scattered I-long dot product on the
+    # vector ALU (fp32 FMA: 157 TFLOP/s against 2500 for the bf16 MFMA, 16x),
+    # while the fp8 MFMA could save at most half of L2's MFMA time; the fix-up
+    # pays only if share * 16 < 0.5, i.e. share < 3.1%.
+    assert share * 16 > 0.5, f"flagged share {share:.3%} would make the fix-up pay"
