@@ -140,6 +140,15 @@ struct MegaLaunchArgs {
                                            // blocks an L2 unit waits for; > 0 makes every
                                            // wait give up after max_spins polls, so a test
                                            // drives the bounded wait's timeout report
+    int mfma_fp8 = 0;                      // 1: both GEMMs on gfx950's block-scaled fp8 MFMA
+                                           // (v_mfma_scale_f32_16x16x128_f8f6f4, the
+                                           // reference's fp8 MMA class) instead of the bf16
+                                           // MFMA after an exact conversion.  Faster at large
+                                           // T; its truncating sums put the layer outside
+                                           // the end-to-end bar the default meets (within
+                                           // check.cu's staged tolerances).  Windows > 32
+                                           // rows, two launches (not with fuse_l1l2):
+                                           // kErrUnsupported otherwise.
 };
 
 // Byte offsets of every region inside the workspace (the single-GPU

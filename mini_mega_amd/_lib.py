@@ -28,7 +28,7 @@ class MegaLaunchArgs(ctypes.Structure):
         ("num_experts", c_int), ("topk", c_int), ("hidden", c_int), ("intermediate", c_int),
         ("max_tokens", c_int), ("workspace_bytes", c_i64), ("x_sf", c_vp), ("w1_sf", c_vp),
         ("w2_sf", c_vp), ("ffn_ue8m0", c_int), ("y_bf16", c_vp), ("fuse_l1l2", c_int), ("l2_no_walk", c_int),
-        ("ready_bias", c_int),
+        ("ready_bias", c_int), ("mfma_fp8", c_int),
     ]
 
     def __init__(this, **kw):  # "self" is a field name (the reference's base pointer)

@@ -35,6 +35,8 @@
 // run as two stream-ordered launches, or (gemm_fused_kernel, opt-in) as one
 // launch whose L2 units wait on per-item ready counters (reference:
 // src/compute_big.cuh:1948-1997).
+#include <type_traits>
+
 #include "mm_kernels.h"
 
 // The kernels are written for gfx950 alone (MFMA shapes, buffer-resource
@@ -81,11 +83,11 @@ struct alignas(16) BigSmem {
 // flight while kt+1 is written to LDS; with one (above 12 token tiles, where
 // registers go to accumulators, and a k-step's 4*NT MFMA groups alone cover
 // an L2 hit; measured even with two at T = 8192), kt+1 is loaded during kt.
-template <int W, int NT, int kAux = 0, bool kOpaqueTid = false>
+template <int W, int NT, int kAux = 0, bool kOpaqueTid = false, int kXS = (NT <= 12 ? 2 : 1)>
 struct XLoader {
     static constexpr int kThreads = Geo<W>::kThreads;
     static constexpr int U = (NT * 128 + kThreads - 1) / kThreads;
-    static constexpr int XS = NT <= 12 ? 2 : 1;
+    static constexpr int XS = kXS;
     const uint8_t* base;
     int tid_;   // kOpaqueTid: the thread index, read once per unit through an empty asm
     uint32_t off[U];
@@ -126,6 +128,16 @@ struct XLoader {
 #pragma unroll
         for (int u = 0; u < U; ++u)
             commit_chunk(&sm.x[stage][0], rs, u, sm.sfx[row_of(chunk(u))][kt]);
+    }
+    // fp8 MFMA path: the chunk's 16 raw bytes go to the fp8 token tile in the
+    // weight-tile layout ([half][lane][16 B], 2 KiB a tile), unconverted (the
+    // MFMA applies the row scale).
+    __device__ __forceinline__ static int slot_of_f8(int i) {
+        const int r = row_of(i), cc = cc_of(i);
+        return (r >> 4) * kTileBytes + (cc & 1) * 1024 + ((r & 15) + 16 * (cc >> 1)) * 16;
+    }
+    __device__ __forceinline__ void commit_chunk_f8(uint8_t* xw, int rs, int u) {
+        *reinterpret_cast<v4i*>(xw + slot_of_f8(chunk(u))) = reg[rs][u];
     }
 };
 
@@ -372,6 +384,144 @@ __device__ __forceinline__ void big_mainloop(v4f (&acc)[Geo<W>::kWT][NT], BigSme
     big_tail<W, NT, S, 0>(acc, sm, xl, w, wt, a0, KF, KT, nx);
 }
 
+// ---------------------------------------------------------- fp8 MFMA path --
+// Opt-in (MegaLaunchArgs::mfma_fp8): both GEMMs on gfx950's block-scaled fp8
+// MFMA, v_mfma_scale_f32_16x16x128_f8f6f4, one instruction per (weight tile,
+// token tile, 128-k step), the UE8M0 bytes as its scale operands (the
+// weight tile's byte from every lane, each token row's byte from its lane).
+// Weights go from the register stages to the MFMA as they are loaded; token
+// rows are committed to LDS unconverted (fp8 tiles of 2 KiB).  Its sums
+// truncate (~2^-20 of sum|terms|; see the probes in tests), so it is outside
+// the end-to-end bar the default bf16 path meets; it is the reference's
+// arithmetic class (its own fp8 MMA, src/compute.cuh:414-417,593-596).
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v4f mfma_f8(const v8i& a, const v8i& b, uint32_t sa, uint32_t sb,
+                                       const v4f& c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, (int)sa, 0,
+                                                            (int)sb);
+}
+
+// Weight register stages of the fp8 path: 2 above 8 token tiles, 4 up to 8.
+// Measured on MI355X at T = 8192 (layer, fp8 path): three stages with one
+// activation stage above 8 tiles 3722-3726 us, four 3814 us, against 3360-
+// 3364 us; T = 2048 even or slower.
+template <int NT>
+constexpr int big_stages_f8() { return NT > 8 ? 2 : 4; }
+
+// The fp8 path's weight stage: each tile's two 16-byte halves loaded straight
+// into one 8-register operand.
+template <int WT>
+struct WStage8 {
+    v8i a[WT];
+};
+
+template <int WT>
+__device__ __forceinline__ void w_load8(WStage8<WT>& w, const WTiles<WT>& wt, int kt) {
+#pragma unroll
+    for (int t = 0; t < WT; ++t) {
+        const int o = (int)wt.lane16, so = kt * kTileBytes;
+        const v4i lo = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o, so);
+        const v4i hi = load16_row_stream(wt.row[t], wt.KT * kTileBytes, o + 1024, so);
+        w.a[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+}
+
+// One k-step: NT chunks, chunk j = token tile j: the LDS read of the operand
+// D tiles ahead (two 16-byte halves and its row scale), a share of the
+// commit of k-step kt+1 (spread over all chunks: the rows were loaded a step
+// earlier; measured even with the second half or last quarter, and the only
+// placement without spills in L1), and kWT MFMAs.
+template <int W, int NT, int S, int s, class XL>
+__device__ __forceinline__ void big_step_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm, XL& xl,
+                                            WStage8<Geo<W>::kWT> (&w)[S],
+                                            const WTiles<Geo<W>::kWT>& wt, int kt, int KT) {
+    constexpr int kWT = Geo<W>::kWT;
+    constexpr int XS = XL::XS, U = XL::U;
+    constexpr int D = NT < 2 ? NT : 2;
+    constexpr int rs = XS == 2 ? ((s + 1) & 1) : 0;
+    const int lane = xl.tid() & 63, wave = xl.wave();
+    w_load8<kWT>(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));
+    xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
+    const uint32_t sc = w_scales<kWT>(sm, kt, wave);
+    uint32_t xro = (kt & 1) * (uint32_t)sizeof(sm.x[0]) + lane * 16;
+    uint32_t xwo = ((kt + 1) & 1) * (uint32_t)sizeof(sm.x[0]);
+    uint32_t sfo = (lane & 15) * kSfxPitch + kt;
+    asm volatile("" : "+v"(xro), "+v"(xwo), "+v"(sfo));
+    const uint8_t* xb = &sm.x[0][0] + xro;
+    uint8_t* xw = &sm.x[0][0] + xwo;
+    const uint8_t* sf = &sm.sfx[0][0] + sfo;
+    v8i b[D + 1];
+    uint32_t bs[D + 1];
+    auto rd = [&](int d, int j) {
+        const v4i lo = *reinterpret_cast<const v4i*>(xb + j * kTileBytes);
+        const v4i hi = *reinterpret_cast<const v4i*>(xb + j * kTileBytes + 1024);
+        b[d] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        bs[d] = sf[j * 16 * kSfxPitch];
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) rd(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        if (j + D < NT) rd((j + D) % (D + 1), j + D);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (j == (u * NT) / U) xl.commit_chunk_f8(xw, rs, u);
+#pragma unroll
+        for (int t = 0; t < kWT; ++t)
+            acc[t][j] = mfma_f8(w[s].a[t], b[j % (D + 1)], (sc >> (8 * t)) & 0xffu,
+                                bs[j % (D + 1)], acc[t][j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+}
+
+template <int W, int NT, int S, int s, class XL>
+__device__ __forceinline__ void big_group_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm, XL& xl,
+                                             WStage8<Geo<W>::kWT> (&w)[S],
+                                             const WTiles<Geo<W>::kWT>& wt, int kb, int KT) {
+    big_step_f8<W, NT, S, s>(acc, sm, xl, w, wt, kb + s, KT);
+    if constexpr (s + 1 < S) big_group_f8<W, NT, S, s + 1>(acc, sm, xl, w, wt, kb, KT);
+}
+
+template <int W, int NT, int S, int r, class XL>
+__device__ __forceinline__ void big_tail_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm, XL& xl,
+                                            WStage8<Geo<W>::kWT> (&w)[S],
+                                            const WTiles<Geo<W>::kWT>& wt, int KF, int KT) {
+    if (KF + r < KT) {
+        big_step_f8<W, NT, S, r>(acc, sm, xl, w, wt, KF + r, KT);
+        if constexpr (r + 2 < S) big_tail_f8<W, NT, S, r + 1>(acc, sm, xl, w, wt, KF, KT);
+    }
+}
+
+// The fp8 path's main loop (big_mainloop's structure, no operand conversion).
+template <int W, int NT, int S, bool kEarly, class XL>
+__device__ __forceinline__ void big_mainloop_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm,
+                                                XL& xl, const WTiles<Geo<W>::kWT>& wt, int KT,
+                                                WStage8<Geo<W>::kWT> (&w)[S]) {
+    constexpr int kWT = Geo<W>::kWT;
+    constexpr int XS = XL::XS, U = XL::U;
+    static_assert(XS == 1 || S % 2 == 0, "two activation stages alternate within a group");
+#pragma unroll
+    for (int t = 0; t < kWT; ++t)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    xl.issue(0, 0);
+    if constexpr (XS == 2) xl.issue(min(1, KT - 1), 1);
+    if constexpr (!kEarly) {
+#pragma unroll
+        for (int st = 0; st < S - 1; ++st) w_load8<kWT>(w[st], wt, min(st, KT - 1));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) xl.commit_chunk_f8(&sm.x[0][0], 0, u);
+    __syncthreads();
+    const int KF = KT - KT % S;
+#pragma unroll 1
+    for (int kb = 0; kb < KF; kb += S) big_group_f8<W, NT, S, 0>(acc, sm, xl, w, wt, kb, KT);
+    big_tail_f8<W, NT, S, 0>(acc, sm, xl, w, wt, KF, KT);
+}
+
 // Per-unit context shared by the two kernels.
 struct BigItem {
     int e, m0, rows, bx, item;   // m0: first slot (absolute)
@@ -568,7 +718,7 @@ __device__ __forceinline__ int l1_tile_row(int bx, int bt, int G) {
 // release below has few dirty L2 lines to write back), every wave waits for
 // its stores, and after the workgroup barrier one thread bumps the item's
 // ready counter with an agent-scope release; the L2 side acquires it.
-template <int W, int NT, bool kFused, class ScalesF>
+template <int W, int NT, bool kFused, bool kF8, class ScalesF>
 __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
                                             ScalesF stage_scales) {
     constexpr int kWT = Geo<W>::kWT, kH = kWT / 2;
@@ -579,7 +729,7 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
         else
             *reinterpret_cast<uint32_t*>(dst) = v;
     };
-    constexpr int S = big_stages<W, NT, false>();
+    constexpr int S = kF8 ? big_stages_f8<NT>() : big_stages<W, NT, false>();
     constexpr bool kEarly = NT <= kEarlyMaxTiles;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, G = p.G, KT = H >> 7;
@@ -588,14 +738,27 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
     wt.KT = KT;
 #pragma unroll
     for (int t = 0; t < kWT; ++t) wt.set(t, we, l1_tile_row<W>(it.bx, kWT * wave + t, G) >> 4, lane);
-    WStage<kWT> w[S];
-    if constexpr (kEarly) w_prologue<kWT, S>(w, wt, KT);
+    std::conditional_t<kF8, WStage8<kWT>, WStage<kWT>> w[S];
+    if constexpr (kEarly) {
+        if constexpr (kF8) {
+#pragma unroll
+            for (int st = 0; st < S - 1; ++st) w_load8<kWT>(w[st], wt, min(st, KT - 1));
+        } else {
+            w_prologue<kWT, S>(w, wt, KT);
+        }
+    }
     stage_scales();
-    XLoader<W, NT> xl;
+    // the fp8 path keeps two activation register stages at every tile count
+    // (measured on MI355X at T = 8192: layer 3267-3269 vs 3399-3417 us with
+    // one stage above 10 tiles)
+    XLoader<W, NT, 0, false, (kF8 || NT <= 12 ? 2 : 1)> xl;
     xl.base = p.x;
     big_loader_init(xl, [&](int r) { return sm.tok[r] * (uint32_t)H; });
     v4f acc[kWT][NT];
-    big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
+    if constexpr (kF8)
+        big_mainloop_f8<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
+    else
+        big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
 
     // h = silu(g) * u: hidden column hw + 16c + 4*(L/16) + i, token 16*j + L%16
     const int hw = it.bx * kL1BlockH + wave * (kL1BlockH / W);
@@ -675,7 +838,7 @@ __device__ __forceinline__ void l1_big_body(const GemmParams& p, const BigItem& 
 // NT (the item's token tiles) is uniform over the block, so every wave runs
 // the same body and the same barriers.
 // Workgroup L of the `grid` L1 workgroups.
-template <int W, bool kFused>
+template <int W, bool kFused, bool kF8 = false>
 __device__ __forceinline__ void l1_big(const GemmParams& p, BigSmem& sm, int* s_unit, int L,
                                        int grid) {
     BigItem it;
@@ -698,7 +861,7 @@ __device__ __forceinline__ void l1_big(const GemmParams& p, BigSmem& sm, int* s_
                 return p.w_sf + ((size_t)it.e * (2 * I / 128) + (rho >> 7)) * KT;
             });
     };
-#define MM_L1_BODY(n) l1_big_body<W, n, kFused>(p, it, sm, stage_scales)
+#define MM_L1_BODY(n) l1_big_body<W, n, kFused, kF8>(p, it, sm, stage_scales)
     MM_BIG_DISPATCH(MM_L1_BODY)
 #undef MM_L1_BODY
 }
@@ -707,6 +870,12 @@ __global__ void __launch_bounds__(512) l1_big_kernel(GemmParams p) {
     __shared__ BigSmem sm;
     __shared__ int s_unit;
     l1_big<8, false>(p, sm, &s_unit, blockIdx.x, gridDim.x);
+}
+
+__global__ void __launch_bounds__(512) l1_big_f8_kernel(GemmParams p) {
+    __shared__ BigSmem sm;
+    __shared__ int s_unit;
+    l1_big<8, false, true>(p, sm, &s_unit, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------------- L2 --
@@ -750,11 +919,11 @@ __device__ __forceinline__ void l2_store_tile(const GemmParams& p, const BigItem
 
 // kFused: the item's ffn rows come from L1 units of the same launch, read at
 // device scope (the caller's stage_scales waits for them first).
-template <int W, int NT, bool kFused, class ScalesF>
+template <int W, int NT, bool kFused, bool kF8, class ScalesF>
 __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& it, BigSmem& sm,
                                             ScalesF stage_scales) {
     constexpr int kWT = Geo<W>::kWT;
-    constexpr int S = big_stages<W, NT, true>();
+    constexpr int S = kF8 ? big_stages_f8<NT>() : big_stages<W, NT, true>();
     constexpr bool kEarly = NT <= kEarlyMaxTiles;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = p.H, I = p.I, KT = I >> 7;
@@ -764,16 +933,26 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     wt.KT = KT;
 #pragma unroll
     for (int t = 0; t < kWT; ++t) wt.set(t, we, (n0 >> 4) + t, lane);
-    WStage<kWT> w[S];
-    if constexpr (kEarly) w_prologue<kWT, S>(w, wt, KT);
+    std::conditional_t<kF8, WStage8<kWT>, WStage<kWT>> w[S];
+    if constexpr (kEarly) {
+        if constexpr (kF8) {
+#pragma unroll
+            for (int st = 0; st < S - 1; ++st) w_load8<kWT>(w[st], wt, min(st, KT - 1));
+        } else {
+            w_prologue<kWT, S>(w, wt, KT);
+        }
+    }
     stage_scales();
-    XLoader<W, NT, kFused ? kBufferSc1 : 0> xl;
+    XLoader<W, NT, kFused ? kBufferSc1 : 0, false, (kF8 || NT <= 12 ? 2 : 1)> xl;
     xl.base = p.x;
     big_loader_init(xl, [&](int r) {
         return (uint32_t)(it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
     });
     v4f acc[kWT][NT];
-    big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
+    if constexpr (kF8)
+        big_mainloop_f8<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
+    else
+        big_mainloop<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
     l2_store_tile<W, NT>(p, it, sm, acc, it.bx * kL2BlockN, lane, wave);
 }
 
@@ -785,7 +964,7 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
 // After the poll, an agent-scope acquire fence pairs with the L1 units'
 // release increments, and the workgroup barrier carries it to every wave;
 // the rows are then read with sc1 (device-coherent) loads.
-template <int W, bool kFused>
+template <int W, bool kFused, bool kF8 = false>
 __device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_unit, int L,
                                        int grid) {
     BigItem it;
@@ -824,7 +1003,7 @@ __device__ __forceinline__ void l2_big(const GemmParams& p, BigSmem& sm, int* s_
                 return p.w_sf + ((size_t)it.e * (H / 128) + (n >> 7)) * KT;
             });
     };
-#define MM_L2_BODY(n) l2_big_body<W, n, kFused>(p, it, sm, stage_scales)
+#define MM_L2_BODY(n) l2_big_body<W, n, kFused, kF8>(p, it, sm, stage_scales)
     MM_BIG_DISPATCH(MM_L2_BODY)
 #undef MM_L2_BODY
 }
@@ -834,6 +1013,12 @@ __global__ void __launch_bounds__(512) l2_big_kernel(GemmParams p) {
     __shared__ int s_unit;
     if (walk_taken(p)) return;   // the walk (launched just before) ran the units
     l2_big<8, false>(p, sm, &s_unit, blockIdx.x, gridDim.x);
+}
+
+__global__ void __launch_bounds__(512) l2_big_f8_kernel(GemmParams p) {
+    __shared__ BigSmem sm;
+    __shared__ int s_unit;
+    l2_big<8, false, true>(p, sm, &s_unit, blockIdx.x, gridDim.x);
 }
 
 // ------------------------------------------------------------- L2 walker --

@@ -95,6 +95,8 @@ int bind(const MegaLaunchArgs& a, Bound& b, bool need_weights) {
     if ((a.ffn_ue8m0 != 0) != any_sf) return kErrUnsupported;
     b.L = layout(a.max_tokens, a.topk, a.num_experts, a.hidden, a.intermediate, a.win_cap);
     if (a.workspace_bytes < b.L.total) return kErrWorkspace;
+    // the fp8 MFMA path exists for the LDS-staged kernels and two launches
+    if (a.mfma_fp8 && (a.fuse_l1l2 || b.L.m_tile <= 32)) return kErrUnsupported;
     b.ws = reinterpret_cast<uint8_t*>(a.rwk);
     b.x = a.self + a.x_off;
     b.x_sf = a.x_sf;
@@ -225,7 +227,8 @@ int do_l1(const MegaLaunchArgs& a, hipStream_t s) {
     p.queue = at<int>(b, b.L.status) + mm::kQueueL1;
     p.tail_ord = reinterpret_cast<const uint8_t*>(p.status + mm::kTailOrdL1);
     const int nb = a.intermediate / mm::kL1BlockH;
-    launch_gemm(kL1Small, mm::l1_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
+    launch_gemm(kL1Small, a.mfma_fp8 ? mm::l1_big_f8_kernel : mm::l1_big_kernel, b.m_tile, nb,
+                b.L.max_items, s, p);
     return launched(kOk);
 }
 
@@ -253,14 +256,15 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     // 1846-1847 us (L2 613 vs 645-646); Zipf(1.1) T = 2048 and T = 8192 even
     // (the one-unit kernel runs them).
     const int64_t pairs = (int64_t)a.tokens * a.topk;
-    if (b.m_tile > 32 && !a.l2_no_walk && pairs > 16LL * a.num_experts &&
+    if (b.m_tile > 32 && !a.l2_no_walk && !a.mfma_fp8 && pairs > 16LL * a.num_experts &&
         pairs <= 128LL * a.num_experts) {
         p.walk = 1;
         // at least one workgroup per XCD range (workgroup L walks range L % 8)
         const int walkers = cu_count() < 8 ? 8 : cu_count();
         hipLaunchKernelGGL(mm::l2_walk_kernel, dim3(walkers), dim3(mm::kBigThreads), 0, s, p);
     }
-    launch_gemm(kL2Small, mm::l2_big_kernel, b.m_tile, nb, b.L.max_items, s, p);
+    launch_gemm(kL2Small, a.mfma_fp8 ? mm::l2_big_f8_kernel : mm::l2_big_kernel, b.m_tile, nb,
+                b.L.max_items, s, p);
     return launched(kOk);
 }
 
@@ -596,6 +600,8 @@ void dump_kernel_resources() {
     print_attr("l2_kernel<1>", (const void*)mm::l2_kernel<1>);
     print_attr("l2_kernel<2>", (const void*)mm::l2_kernel<2>);
     print_attr("l2_big_kernel", (const void*)mm::l2_big_kernel);
+    print_attr("l1_big_f8_kernel", (const void*)mm::l1_big_f8_kernel);
+    print_attr("l2_big_f8_kernel", (const void*)mm::l2_big_f8_kernel);
     print_attr("l2_walk_kernel", (const void*)mm::l2_walk_kernel);
     print_attr("gemm_fused_kernel", (const void*)mm::gemm_fused_kernel);
     print_attr("combine<cached rows>", (const void*)mm::combine_kernel<false>);
@@ -642,7 +648,7 @@ long long mm_args_offset(const char* f) {
     MM_FIELD(hidden) MM_FIELD(intermediate) MM_FIELD(max_tokens) MM_FIELD(workspace_bytes)
     MM_FIELD(x_sf) MM_FIELD(w1_sf) MM_FIELD(w2_sf) MM_FIELD(ffn_ue8m0) MM_FIELD(y_bf16)
     MM_FIELD(fuse_l1l2)
-    MM_FIELD(l2_no_walk) MM_FIELD(ready_bias)
+    MM_FIELD(l2_no_walk) MM_FIELD(ready_bias) MM_FIELD(mfma_fp8)
 #undef MM_FIELD
     return -1;
 }

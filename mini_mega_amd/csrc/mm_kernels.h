@@ -100,6 +100,8 @@ template <int MT> __global__ void l1_kernel(GemmParams p);
 template <int MT> __global__ void l2_kernel(GemmParams p);
 __global__ void l1_big_kernel(GemmParams p);
 __global__ void l2_big_kernel(GemmParams p);
+__global__ void l1_big_f8_kernel(GemmParams p);   // MegaLaunchArgs::mfma_fp8
+__global__ void l2_big_f8_kernel(GemmParams p);
 __global__ void l2_walk_kernel(GemmParams p);
 __global__ void gemm_fused_kernel(GemmParams p1, GemmParams p2, int g1);
 

@@ -135,6 +135,9 @@ class SymmBuffer:
         # L2 as a walk of one workgroup per CU where the items allow it
         # (MegaLaunchArgs::l2_no_walk = 0)
         self.l2_walk = True
+        # both GEMMs on the block-scaled fp8 MFMA (MegaLaunchArgs::mfma_fp8):
+        # faster at large batches, outside the end-to-end bar of the default
+        self.mfma_fp8 = False
         self.launch_count = 0
 
     # -- workspace views (staged parity checks read these, as check.cu dumps
@@ -209,6 +212,7 @@ class SymmBuffer:
         a.skip_prologue = int(skip_prologue)
         a.fuse_l1l2 = int(bool(self.fuse_l1l2))
         a.l2_no_walk = int(not self.l2_walk)
+        a.mfma_fp8 = int(bool(self.mfma_fp8))
         a.num_experts, a.topk = self.num_experts, self.num_topk
         a.hidden, a.intermediate = self.hidden, self.intermediate_hidden
         a.max_tokens = self.num_max_tokens_per_rank
