@@ -441,7 +441,7 @@ __device__ __forceinline__ void big_step_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem
     constexpr int D = NT < 2 ? NT : 2;
     constexpr int rs = XS == 2 ? ((s + 1) & 1) : 0;
     const int lane = xl.tid() & 63, wave = xl.wave();
-    w_load8<kWT>(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));
+    w_load8<kWT>(w[(s + S - 1) % S], wt, min(kt + S - 1, KT - 1));   // s: step in the group
     xl.issue(min(kt + XS, KT - 1), XS == 2 ? (s & 1) : 0);
     const uint32_t sc = w_scales<kWT>(sm, kt, wave);
     uint32_t xro = (kt & 1) * (uint32_t)sizeof(sm.x[0]) + lane * 16;
@@ -470,28 +470,30 @@ __device__ __forceinline__ void big_step_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem
             if (j == (u * NT) / U) xl.commit_chunk_f8(xw, rs, u);
 #pragma unroll
         for (int t = 0; t < kWT; ++t)
-            acc[t][j] = mfma_f8(w[s].a[t], b[j % (D + 1)], (sc >> (8 * t)) & 0xffu,
+            acc[t][j] = mfma_f8(w[s % S].a[t], b[j % (D + 1)], (sc >> (8 * t)) & 0xffu,
                                 bs[j % (D + 1)], acc[t][j]);
         __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 }
 
-template <int W, int NT, int S, int s, class XL>
+// A group of GS k-steps (a multiple of S, and even with two activation
+// register stages), so that both stage indices are static within it.
+template <int W, int NT, int S, int GS, int s, class XL>
 __device__ __forceinline__ void big_group_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm, XL& xl,
                                              WStage8<Geo<W>::kWT> (&w)[S],
                                              const WTiles<Geo<W>::kWT>& wt, int kb, int KT) {
     big_step_f8<W, NT, S, s>(acc, sm, xl, w, wt, kb + s, KT);
-    if constexpr (s + 1 < S) big_group_f8<W, NT, S, s + 1>(acc, sm, xl, w, wt, kb, KT);
+    if constexpr (s + 1 < GS) big_group_f8<W, NT, S, GS, s + 1>(acc, sm, xl, w, wt, kb, KT);
 }
 
-template <int W, int NT, int S, int r, class XL>
+template <int W, int NT, int S, int GS, int r, class XL>
 __device__ __forceinline__ void big_tail_f8(v4f (&acc)[Geo<W>::kWT][NT], BigSmem& sm, XL& xl,
                                             WStage8<Geo<W>::kWT> (&w)[S],
                                             const WTiles<Geo<W>::kWT>& wt, int KF, int KT) {
     if (KF + r < KT) {
         big_step_f8<W, NT, S, r>(acc, sm, xl, w, wt, KF + r, KT);
-        if constexpr (r + 2 < S) big_tail_f8<W, NT, S, r + 1>(acc, sm, xl, w, wt, KF, KT);
+        if constexpr (r + 2 < GS) big_tail_f8<W, NT, S, GS, r + 1>(acc, sm, xl, w, wt, KF, KT);
     }
 }
 
@@ -502,7 +504,7 @@ __device__ __forceinline__ void big_mainloop_f8(v4f (&acc)[Geo<W>::kWT][NT], Big
                                                 WStage8<Geo<W>::kWT> (&w)[S]) {
     constexpr int kWT = Geo<W>::kWT;
     constexpr int XS = XL::XS, U = XL::U;
-    static_assert(XS == 1 || S % 2 == 0, "two activation stages alternate within a group");
+    constexpr int GS = (XS == 2 && S % 2) ? 2 * S : S;
 #pragma unroll
     for (int t = 0; t < kWT; ++t)
 #pragma unroll
@@ -516,10 +518,10 @@ __device__ __forceinline__ void big_mainloop_f8(v4f (&acc)[Geo<W>::kWT][NT], Big
 #pragma unroll
     for (int u = 0; u < U; ++u) xl.commit_chunk_f8(&sm.x[0][0], 0, u);
     __syncthreads();
-    const int KF = KT - KT % S;
+    const int KF = KT - KT % GS;
 #pragma unroll 1
-    for (int kb = 0; kb < KF; kb += S) big_group_f8<W, NT, S, 0>(acc, sm, xl, w, wt, kb, KT);
-    big_tail_f8<W, NT, S, 0>(acc, sm, xl, w, wt, KF, KT);
+    for (int kb = 0; kb < KF; kb += GS) big_group_f8<W, NT, S, GS, 0>(acc, sm, xl, w, wt, kb, KT);
+    big_tail_f8<W, NT, S, GS, 0>(acc, sm, xl, w, wt, KF, KT);
 }
 
 // Per-unit context shared by the two kernels.
