@@ -935,6 +935,7 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     wt.KT = KT;
 #pragma unroll
     for (int t = 0; t < kWT; ++t) wt.set(t, we, (n0 >> 4) + t, lane);
+    v4f acc[kWT][NT];
     std::conditional_t<kF8, WStage8<kWT>, WStage<kWT>> w[S];
     if constexpr (kEarly) {
         if constexpr (kF8) {
@@ -950,7 +951,6 @@ __device__ __forceinline__ void l2_big_body(const GemmParams& p, const BigItem& 
     big_loader_init(xl, [&](int r) {
         return (uint32_t)(it.m0 + (r < it.rows ? r : 0)) * (uint32_t)I;
     });
-    v4f acc[kWT][NT];
     if constexpr (kF8)
         big_mainloop_f8<W, NT, S, kEarly>(acc, sm, xl, wt, KT, w);
     else
