@@ -885,8 +885,12 @@ __global__ void __launch_bounds__(512) l1_big_f8_kernel(GemmParams p) {
 // that every global store writes whole rows (a wave: two 512-byte rows per
 // instruction) instead of 32-byte pieces of 16 rows from the MFMA layout.
 // The caller's main loop ended on a barrier; the tile (<= 256 rows at a
-// 544-byte pitch, 136 KiB) overlays the LDS operand tiles and the scales.
-constexpr int kL2TilePitch = kL2BlockN * 2 + 32;
+// 528-byte pitch, 132 KiB) overlays the LDS operand tiles and the scales.
+// The pitch is 132 dwords, 4 banks past a multiple of 64: the 16 rows of a
+// quarter-wave's 8-byte writes fall in distinct banks (measured on MI355X at
+// T = 8192 / 2048: L2's LDS bank conflicts halved against a 544-byte pitch,
+// bf16 L2 1561 vs 1569-1570 us, fp8 L2 1071-1075 vs 1078-1089 us).
+constexpr int kL2TilePitch = kL2BlockN * 2 + 16;
 static_assert(kBigRows * kL2TilePitch <= (int)sizeof(BigSmem), "L2 store tile");
 template <int W, int NT>
 __device__ __forceinline__ void l2_store_tile(const GemmParams& p, const BigItem& it, BigSmem& sm,
