@@ -100,6 +100,7 @@ struct MegaLaunchArgs {
     int64_t x_off = 0, weights_off = 0;    // x = self + x_off, w = self + weights_off
     int in_bf16 = 0;                       // x is bf16 [tokens][H] (folded to fp8)
     int skip_combine = 0;                  // diagnostic: launch_reduce does nothing
+                                           // (also while MX_SKIP_COMBINE != 0)
 
     // [3] output
     float* y = nullptr;                    // [tokens][H] fp32 (may be null if y_bf16)
@@ -193,8 +194,11 @@ void launch_compute(const MegaLaunchArgs& a, hipStream_t stream);
 void launch_l1(const MegaLaunchArgs& a, hipStream_t stream);
 void launch_l2(const MegaLaunchArgs& a, hipStream_t stream);
 // Top-k weighted reduce into y / y_bf16 (reference: launch_reduce, :128).
+// Does nothing while the environment has MX_SKIP_COMBINE != 0 (read at each
+// launch, as the reference reads it: src/megakernel.cu:137-139).
 void launch_reduce(const MegaLaunchArgs& a, hipStream_t stream);
 // launch_compute + launch_reduce on one stream (reference: launch_full, :130).
+// While MX_SKIP_REDUCE != 0, launch_compute only (src/megakernel.cu:255-258).
 void launch_full(const MegaLaunchArgs& a, hipStream_t stream);
 // Empty kernel (launch floor; reference: launch_empty, :132).
 void launch_empty(int grid, int threads, int64_t smem, hipStream_t stream);

@@ -9,6 +9,7 @@
 // is caller-owned, or (mm_launch_full_noalloc) the file-scope `scratch`.
 #include <cstddef>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -268,13 +269,22 @@ int do_l2(const MegaLaunchArgs& a, hipStream_t s) {
     return launched(kOk);
 }
 
+// The reference's diagnostic switches, read at every launch as it reads them
+// (src/megakernel.cu:137-139,255-258): MX_SKIP_COMBINE != 0 acts as
+// skip_combine (launch_reduce does nothing), MX_SKIP_REDUCE != 0 makes
+// launch_full skip its reduce (compute only).
+bool env_on(const char* name) {
+    const char* v = std::getenv(name);
+    return v != nullptr && std::atoi(v) != 0;
+}
+
 int do_reduce(const MegaLaunchArgs& a, hipStream_t s) {
     Bound b;
     int st = bind(a, b, false);
     if (st != kOk) return st;
     // an empty batch writes nothing, so it needs no output (a (0, H) tensor
     // has a null data pointer)
-    if (a.skip_combine || a.tokens == 0) return kOk;
+    if (a.skip_combine || a.tokens == 0 || env_on("MX_SKIP_COMBINE")) return kOk;
     if (a.y == nullptr && a.y_bf16 == nullptr) return kErrNullPointer;
     // a token per workgroup (H / 8 threads, whole waves) up to 1024 threads
     const int threads = a.hidden / 8 <= 1024 ? (a.hidden / 8 + 63) / 64 * 64 : 256;
@@ -360,7 +370,7 @@ int do_compute(const MegaLaunchArgs& a, hipStream_t s) {
 
 int do_full(const MegaLaunchArgs& a, hipStream_t s) {
     int st = do_compute(a, s);
-    if (st == kOk) st = do_reduce(a, s);
+    if (st == kOk && !env_on("MX_SKIP_REDUCE")) st = do_reduce(a, s);
     return st;
 }
 

@@ -1,8 +1,8 @@
 """GPU tests of the operator API around the layer: the split compute / reduce
-pair, skip_prologue (alone and as graph nodes), empty batches, output checks
-and the device status words.  Every result is compared bit for bit with the
-plain full-layer launch of the same inputs, which the parity tests check
-against the oracle."""
+pair, the reference's launch-time switches, skip_prologue (alone and as graph
+nodes), empty batches, output checks and the device status words.  Every
+result is compared bit for bit with the plain full-layer launch of the same
+inputs, which the parity tests check against the oracle."""
 import ctypes
 import sys
 
@@ -74,6 +74,35 @@ def test_split_compute_reduce_equals_full_layer():
     mm.fp8_mega_moe_reduce(y5, buf)
     torch.cuda.synchronize()
     assert torch.equal(y5, y_full[:5])
+
+
+def test_reference_env_switches_skip_the_reduce(monkeypatch):
+    """The reference's launch-time switches (src/megakernel.cu:137-139,255-258):
+    MX_SKIP_REDUCE=1 makes launch_full run the compute only, MX_SKIP_COMBINE=1
+    makes launch_reduce a no-op; without them the reduce of that computed
+    routing gives the full layer's output."""
+    _say("MX_SKIP_REDUCE / MX_SKIP_COMBINE")
+    L = mm.lib()
+    E, K, H, I, T = 32, 8, 1024, 512, 96
+    c = mc.normal_case(E, K, H, I, T, seed=93, scaled=True)
+    buf = mm.get_symm_buffer_for_mega_moe(None, E, T, K, H, I)
+    _load(buf, c)
+    y_full = _full(buf, c)
+    y = torch.full((T, H), 7.0, dtype=torch.bfloat16, device="cuda")
+    a = buf.make_args(T, (c.w1, c.s1), (c.w2, c.s2), y_bf16=y)
+    monkeypatch.setenv("MX_SKIP_REDUCE", "1")
+    assert L.mm_launch_full(ctypes.byref(a), _stream()) == 0
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all()), "launch_full reduced under MX_SKIP_REDUCE=1"
+    monkeypatch.delenv("MX_SKIP_REDUCE")
+    monkeypatch.setenv("MX_SKIP_COMBINE", "1")
+    assert L.mm_launch_reduce(ctypes.byref(a), _stream()) == 0
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all()), "launch_reduce wrote y under MX_SKIP_COMBINE=1"
+    monkeypatch.setenv("MX_SKIP_COMBINE", "0")
+    assert L.mm_launch_reduce(ctypes.byref(a), _stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_full)
 
 
 def test_split_reduce_rejects_bad_calls():
