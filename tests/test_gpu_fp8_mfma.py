@@ -51,6 +51,7 @@ def _run_f8(c):
     (32, 8, 1024, 768, 200, None, 128, False),
     (8, 8, 768, 512, 1200, None, 0, True),     # 15-tile items: one activation stage
     (256, 8, 6144, 2048, 512, None, 0, True),
+    (256, 8, 6144, 2048, 2048, 1.1, 0, True),    # skewed: hot experts in several items
     (256, 8, 6144, 2048, 8192, None, 0, True),
 ])
 def test_fp8_mfma_layer_at_checkcu_tolerances(E, K, H, I, T, zipf, win, scaled):
